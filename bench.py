@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X block-quantized Linear path (one JSON line).
+
+Headline (`value`): q4_0 decode GEMV at the Qwen2-7B FFN-up shape
+(W [18944, 3584], M = 1) in algorithmic HBM GB/s:
+bytes = N*ceil(K/32)*18 + 4*M*K + 4*M*N per call. A step is one call on one
+activation vector. Weights rotate over >= 512 MB of distinct device copies so
+every call streams its weight from HBM (MI355X has a 256 MB Infinity Cache).
+The timed launches are captured in one HIP graph and bracketed by HIP events
+on the stream they run on.
+
+Also reported in the same line: the q8_0 prefill GEMM (configs[4], M=512,
+W [11008, 4096]) in TFLOP/s against the dense fp16 MFMA peak, and the
+reference CPU path (the oracle restatement) timed on the host cores.
+`--all` adds every BASELINE configuration and the 196-GEMV decode sweep.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+import __graft_entry__ as graft  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 512 << 20
+
+GGUF_BLOCK = {"q8_0": 34, "q4_0": 18, "q4_1": 20}
+
+
+def alg_bytes(qtype, m, n, k):
+    return n * ((k + 31) // 32) * GGUF_BLOCK[qtype] + 4 * m * k + 4 * m * n
+
+
+def alg_flops(m, n, k):
+    return 2 * m * n * k
+
+
+class Case:
+    """One shape: rotated weight copies, fixed activations, output buffer."""
+
+    def __init__(self, pkg, torch, qtype, m, n, k, seed, rotate=True):
+        import mini_llama_amd.synth as synth
+        self.pkg, self.torch = pkg, torch
+        self.qtype, self.m, self.n, self.k = qtype, m, n, k
+        blocks = synth.make_blocks(qtype, n, k, seed)
+        base = pkg.upload(qtype, blocks, n, k, device="cuda")
+        copies = max(1, -(-ROTATE_BYTES // base.nbytes)) if rotate else 1
+        self.weights = [base]
+        for _ in range(copies - 1):
+            buf = base.buffer.clone()
+            self.weights.append(pkg.TiledWeight(qtype, n, k, buf,
+                                                pkg.weight_layout(qtype, n, k)))
+        x = synth.make_x(m, k, seed + 1)
+        self.x = torch.from_numpy(x if m > 1 else x[0]).to("cuda")
+        self.y = torch.empty((m, n) if m > 1 else (n,), dtype=torch.float32,
+                             device="cuda")
+
+    def launch(self, i):
+        self.pkg.linear(self.weights[i % len(self.weights)], self.x, self.y)
+
+
+def time_graph(torch, launch, steps, warmup):
+    """Capture `steps` launches in a HIP graph; return seconds for one replay
+    bracketed by events on the capturing stream (after `warmup` eager and
+    one warm replay)."""
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(max(warmup, 1)):
+            launch(i)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed):
+    log(f"{qtype} m={m} n={n} k={k}: setup")
+    c = Case(pkg, torch, qtype, m, n, k, seed)
+    sec = time_graph(torch, c.launch, steps, warmup)
+    per = sec / steps
+    out = {"qtype": qtype, "m": m, "n": n, "k": k, "copies": len(c.weights),
+           "us_per_call": per * 1e6,
+           "gbs": alg_bytes(qtype, m, n, k) / per / 1e9,
+           "tflops": alg_flops(m, n, k) / per / 1e12}
+    assert torch.isfinite(c.y).all().item()
+    log(f"{qtype} m={m} n={n} k={k}: {out['us_per_call']:.2f} us/call, "
+        f"{out['gbs']:.0f} GB/s, {out['tflops']:.1f} TFLOP/s")
+    del c
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_sweep(pkg, torch, steps, warmup):
+    """28 layers x {q,k,v,o,gate,up,down} q4_0 GEMVs (hidden 3584, FFN 18944,
+    GQA kv 512), M = 1, one fixed x per shape, one graph = one decode step."""
+    import mini_llama_amd.synth as synth
+    shapes = [("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584),
+              ("o", 3584, 3584), ("gate", 18944, 3584), ("up", 18944, 3584),
+              ("down", 3584, 18944)]
+    xs = {kk: torch.from_numpy(synth.make_x(1, kk, 900 + kk)[0]).to("cuda")
+          for kk in (3584, 18944)}
+    ys = {nn: torch.empty(nn, dtype=torch.float32, device="cuda")
+          for nn in (512, 3584, 18944)}
+    layers = []
+    log("sweep: uploading 28 layers")
+    for layer in range(28):
+        layers.append([pkg.upload("q4_0", synth.make_blocks("q4_0", n, k,
+                                                             5000 + 10 * layer + i),
+                                  n, k, device="cuda")
+                       for i, (_, n, k) in enumerate(shapes)])
+    calls = [(w, xs[w.k], ys[w.n]) for lw in layers for w in lw]
+
+    def step(_):
+        for w, x, y in calls:
+            pkg.linear(w, x, y)
+
+    steps = max(1, steps)
+    sec = time_graph(torch, step, steps, warmup) / steps
+    total = sum(alg_bytes("q4_0", 1, w.n, w.k) for w, _, _ in calls)
+    flops = sum(alg_flops(1, w.n, w.k) for w, _, _ in calls)
+    del layers, calls
+    torch.cuda.empty_cache()
+    return {"gemvs": 196, "us_per_step": sec * 1e6, "gbs": total / sec / 1e9,
+            "bytes": total, "tflops": flops / sec / 1e12}
+
+
+def cpu_baseline(qtype, n, k, budget_s=10.0):
+    """The reference CPU path (oracle restatement of linearQ40 with the
+    reference thread partition), timed on this host's cores."""
+    oracle = graft.load_oracle()
+    graft.load_package()
+    import mini_llama_amd.synth as synth
+    threads = max(1, min(16, os.cpu_count() or 1))
+    blocks = synth.make_blocks(qtype, n, k, 1)
+    x = synth.make_x(1, k, 2)[0]
+    oracle.linear(x, blocks, (n, k), qtype, threads=threads)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.linear(x, blocks, (n, k), qtype, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 1000:
+            break
+    per = el / reps
+    return {"value": alg_bytes(qtype, 1, n, k) / per / 1e9, "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{reps} full {qtype} GEMV calls W[{n},{k}] M=1 "
+                      f"({per * 1e3:.2f} ms/call, {threads} threads, "
+                      f"scalar -O2 build of oracle/quant_ref.c)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--all", action="store_true",
+                    help="also run every BASELINE config and the decode sweep")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU leg")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (no multi-GPU path); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    pkg = graft.load_package()
+    pkg.lib()
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+
+    head = bench_case(pkg, torch, "q4_0", 1, 18944, 3584, args.steps,
+                      args.warmup, seed=1000)
+    pre_steps = max(10, min(200, args.steps // 5))
+    prefill = bench_case(pkg, torch, "q8_0", 512, 11008, 4096, pre_steps,
+                         min(args.warmup, 5), seed=4000)
+    result = {
+        "metric": "q-GEMV achieved HBM GB/s (% of 8 TB/s); prefill q8_0 GEMM "
+                  "TOPS (% MFMA)",
+        "value": round(head["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["us_per_call"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights x fp32 activations (fp16 hi/lo MFMA, fp32 accumulate)",
+        "data": "synthetic (seeded; BASELINE.json distributions)",
+        "config": {"workload": "configs[1]: q4_0 GEMV W[18944,3584] M=1 "
+                               "(Qwen2-7B FFN-up), weights rotated over "
+                               f"{head['copies']} HBM copies",
+                   "m": 1, "n": 18944, "k": 3584, "qtype": "q4_0"},
+        "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "prefill": {"workload": "configs[4]: q8_0 GEMM W[11008,4096] x "
+                                "X[512,4096] fp32",
+                    "us_per_call": round(prefill["us_per_call"], 2),
+                    "tflops": round(prefill["tflops"], 1),
+                    "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+                    "frac": round(prefill["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                    "dtype": "fp16 MFMA, fp32 accumulate"},
+    }
+    if args.all:
+        extra = {}
+        for name, qt, m, n, k in [("c0", "q8_0", 1, 4096, 4096),
+                                  ("c2", "q4_1", 1, 4096, 14336),
+                                  ("c3_m4", "q4_0", 4, 4096, 4096),
+                                  ("c3_m16", "q4_0", 16, 4096, 4096),
+                                  ("c3_m64", "q4_0", 64, 4096, 4096)]:
+            r = bench_case(pkg, torch, qt, m, n, k, args.steps, args.warmup, 100)
+            extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
+                           for kk, v in r.items()}
+            extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+        sw = bench_sweep(pkg, torch, max(1, args.steps // 100), 1)
+        sw["frac_hbm"] = round(sw["gbs"] / HBM_PEAK_GBS, 4)
+        extra["sweep"] = {kk: (round(v, 3) if isinstance(v, float) else v)
+                          for kk, v in sw.items()}
+        result["configs"] = extra
+    if not args.no_cpu:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline("q4_0", 18944, 3584, args.cpu_budget)
+        result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 3)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,161 @@
+/*
+ * mlq — MI355X (gfx950) block-quantized Linear for mini-llama: the C ABI.
+ *
+ * Plain C entry points (no C++ or torch types) over hand-written HIP kernels.
+ * They replace the launch layer and kernels of the reference's CUDA quantized
+ * Linear (src/cuda_quant.cu:78-517, include/mini_llama/cuda_quant.h:13-76)
+ * and the raw upload of src/cuda_weight_upload.cc:111-290. The C++ mirror of
+ * the reference interface (hipQ80Linear, ... in mini_llama/hip_quant.h) is
+ * written on top of these.
+ *
+ * Conventions
+ *  - Every entry point returns an mlq_status (0 = success) and never throws.
+ *  - Work is stream-ordered on the given stream (NULL = the null stream);
+ *    nothing here synchronizes unless the name says so.
+ *  - Device pointers are borrowed: the caller owns every buffer.
+ *  - Shapes follow the reference: W is [n = out_features, k = in_features]
+ *    stored as rows of ceil(k/32) GGUF blocks (q8_0 34 B, q4_0 18 B,
+ *    q4_1 20 B; include/mini_llama/quantized_tensor.h:36-72); x is [m, k]
+ *    fp32 row-major, y is [m, n] fp32 row-major. k need not be a multiple of
+ *    32 (the last block of a row is partial, as in src/quant.cc:463-464).
+ */
+#ifndef MLQ_H_
+#define MLQ_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same handle type as HIP's hipStream_t. */
+struct ihipStream_t;
+typedef struct ihipStream_t* mlq_stream_t;
+
+/* Numeric values follow QuantType's enumerator order
+ * (include/mini_llama/quantized_tensor.h:23-28). */
+enum mlq_type { MLQ_F32 = 0, MLQ_Q8_0 = 1, MLQ_Q4_0 = 2, MLQ_Q4_1 = 3 };
+
+enum mlq_status {
+  MLQ_OK = 0,
+  MLQ_ERR_INVALID_ARG = -1,      /* null pointer, unknown type, bad flag   */
+  MLQ_ERR_SHAPE = -2,            /* non-positive dims, in_features mismatch */
+  MLQ_ERR_BLOCK_COUNT = -3,      /* block_count != n * ceil(k/32)          */
+  MLQ_ERR_BUFFER_TOO_SMALL = -4, /* destination/workspace smaller than needed */
+  MLQ_ERR_UNSUPPORTED = -5,      /* shape outside what the kernels accept  */
+  MLQ_ERR_NO_DEVICE = -6,        /* no usable HIP device                   */
+  MLQ_ERR_HIP = -100             /* HIP runtime error, see mlq_last_hip_error */
+};
+
+/* Layout of a repacked ("tiled") weight held in one device allocation.
+ * Rows are grouped in tiles of 16, blocks in groups of 4 (128 k). A (tile,
+ * group) unit is one 64-lane wave line: lane L = n + 16*kq holds quarter kq
+ * (elements 8kq..8kq+7) of each of the 4 blocks of row n, i.e. the B operand
+ * of one v_mfma_f32_16x16x32_f16 per block. With G = ceil(ceil(k/32)/4):
+ *   q4_0/q4_1 quants: 16 B per lane at qs_off + ((t*G+g)*64 + L)*16; word j
+ *                     = block 4g+j; element 8kq+i at nibble i/2 + 4*(i%2)
+ *   q8_0 quants:      32 B per lane as two 16 B lines (h = 0, 1) at
+ *                     qs_off + (((t*G+g)*2+h)*64 + L)*16; words 2u, 2u+1 =
+ *                     block 4g+2h+u; codes stored as q+128; element 4w+i at
+ *                     byte i/2 + 2*(i%2)
+ *   scales d (fp16):  d_off + 2*(((t*G+g)*16 + n)*4 + j) for block 4g+j
+ *   mins m (q4_1):    same indexing from m_off
+ * Padding rows/blocks decode to 0. Sizes come from mlq_weight_layout. */
+typedef struct mlq_weight {
+  void* base;      /* device (or host) allocation holding every region */
+  int32_t type;    /* enum mlq_type (Q8_0, Q4_0, Q4_1)                 */
+  int32_t n;       /* out_features                                      */
+  int32_t k;       /* in_features                                       */
+  int32_t nb;      /* blocks per row = ceil(k/32)                       */
+  uint64_t qs_off; /* byte offset of the quant region                   */
+  uint64_t d_off;  /* byte offset of the fp16 scale region              */
+  uint64_t m_off;  /* byte offset of the fp16 min region (q4_1), else 0 */
+  uint64_t bytes;  /* total bytes of the allocation                     */
+} mlq_weight;
+
+/* ---------------------------------------------------------------------- */
+/* Library / device                                                        */
+/* ---------------------------------------------------------------------- */
+
+/* Human-readable text for an mlq_status. */
+const char* mlq_status_string(int status);
+/* hipError_t of the last MLQ_ERR_HIP returned on this thread (0 if none). */
+int mlq_last_hip_error(void);
+/* Number of visible HIP devices (0 and MLQ_ERR_NO_DEVICE when none).
+ * Replaces cudaDeviceCount (include/mini_llama/cuda_runtime.h:29). */
+int mlq_device_count(int* count);
+/* GGUF block size in bytes for a quant type (34/18/20), 0 for others.
+ * Matches sizeof(BlockQ80/Q40/Q41) (quantized_tensor.h:41-72). */
+size_t mlq_block_bytes(int type);
+
+/* ---------------------------------------------------------------------- */
+/* Weight upload: GGUF AoS blocks -> tiled layout                          */
+/* (replaces the raw AoS copy of src/cuda_weight_upload.cc:111-290)        */
+/* ---------------------------------------------------------------------- */
+
+/* Fill *out with the region offsets and total size of the tiled layout for
+ * an [n, k] weight of `type` (out->base is set to NULL). */
+int mlq_weight_layout(int type, int n, int k, mlq_weight* out);
+
+/* Host-side repack: `aos` holds n*ceil(k/32) GGUF blocks in host memory,
+ * `dst` (host, dst_bytes >= layout bytes) receives the tiled layout.
+ * Validates block_count like uploadQ*LinearWeight
+ * (src/cuda_weight_upload.cc:118-139). */
+int mlq_repack_host(int type, const void* aos, size_t block_count, int n, int k,
+                    void* dst, size_t dst_bytes);
+
+/* Device-side repack of AoS blocks already in device memory into `dst`
+ * (device). Stream-ordered. */
+int mlq_repack_device(int type, const void* aos_dev, size_t block_count, int n,
+                      int k, void* dst_dev, size_t dst_bytes,
+                      mlq_stream_t stream);
+
+/* Dequantize rows [row0, row0+rows) of a tiled weight into fp32 out
+ * [rows, k] (device). Element values are exactly d*q (q8_0), d*(q-8)
+ * (q4_0), d*q+m (q4_1) as fp32, i.e. dequantizeFromQ* (src/quant.cc:192-392).
+ * Used to prove bit-exact dequantization. */
+int mlq_dequantize(const mlq_weight* w, int row0, int rows, float* out,
+                   mlq_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Quantized Linear: y[m, n] = sum_k W[n, k] * x[m, k]                      */
+/* ---------------------------------------------------------------------- */
+
+/* Tiled weight (from the upload path). Picks the kernel family by m:
+ *  m = 1..8 (decode): HBM-streaming GEMV. Codes decode exactly to fp16,
+ *    activations enter as an fp16 hi+lo pair (two MFMA rows), each block's
+ *    MFMA result is scaled by its fp16 scale in fp32: fp32-class accuracy.
+ *  m > 8 (prefill / batched): MFMA f16 GEMM on d*q pre-scaled to fp16 and
+ *    fp16-rounded activations, fp32 accumulation (~1e-4 relative).
+ * Replaces q80/q40/q41LinearKernel + their launchers
+ * (src/cuda_quant.cu:78-182, 300-361, 378-439, 456-517). */
+int mlq_linear(const mlq_weight* w, const float* x, float* y, int m,
+               mlq_stream_t stream);
+
+/* Raw GGUF AoS blocks in device memory: the meaning of the `const void*`
+ * weight of cudaQ*LinearDeviceWeight / cudaQ*LinearDeviceInput
+ * (src/cuda_quant.cu:300-361). The blocks are repacked into `workspace`
+ * (device, >= mlq_weight_layout(...).bytes) and then run through
+ * mlq_linear. */
+int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,
+                   int k, const float* x, float* y, int m, void* workspace,
+                   size_t workspace_bytes, mlq_stream_t stream);
+
+/* Kernel-family overrides for tests and measurement: force the GEMV
+ * (requires m <= 8 and k within its LDS budget, else MLQ_ERR_UNSUPPORTED)
+ * or the GEMM regardless of m. */
+enum mlq_path { MLQ_PATH_AUTO = 0, MLQ_PATH_GEMV = 1, MLQ_PATH_MFMA = 2 };
+int mlq_linear_path(const mlq_weight* w, const float* x, float* y, int m,
+                    int path, mlq_stream_t stream);
+
+/* Add bias[n] to every row of y[m, n] on the device (the reference adds the
+ * bias on the host after download, src/cuda_quant.cu:229-235, 327-329). */
+int mlq_add_bias(float* y, const float* bias, int m, int n,
+                 mlq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLQ_H_ */

@@ -1,0 +1,253 @@
+"""mini-llama HIP backend for MI355X: Python front end of the C ABI (libmlq).
+
+ctypes bindings for ``include/mlq.h``. PyTorch is used only for device
+memory and streams. There is no CPU fallback: every compute entry point runs
+the HIP kernels in ``libmlq.so`` and raises if the library is missing.
+
+The directory name contains a hyphen, so load it with ``load_package()`` from
+the repository root helpers (tests/conftest.py, bench.py, __graft_entry__.py),
+which registers it as ``mini_llama_amd``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmlq.so")
+HOST_LIB_PATH = os.path.join(HERE, "libmini_llama_hip.so")
+CPP_TEST_PATH = os.path.join(HERE, "test_hip_quant")
+
+# enum mlq_type (numeric values follow the reference QuantType order)
+F32, Q8_0, Q4_0, Q4_1 = 0, 1, 2, 3
+TYPES = {"q8_0": Q8_0, "q4_0": Q4_0, "q4_1": Q4_1}
+BLOCK_BYTES = {"q8_0": 34, "q4_0": 18, "q4_1": 20}
+# enum mlq_path
+PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
+GEMV_MAX_ROWS = 8
+
+STATUS = {
+    0: "ok", -1: "invalid argument", -2: "shape mismatch",
+    -3: "block count mismatch", -4: "buffer too small",
+    -5: "unsupported shape", -6: "no HIP device", -100: "HIP runtime error",
+}
+
+
+class MLQError(RuntimeError):
+    def __init__(self, status: int, what: str, hip_error: int = 0):
+        msg = f"{what}: {STATUS.get(status, 'unknown')} ({status})"
+        if status == -100:
+            msg += f", hipError_t {hip_error}"
+        super().__init__(msg)
+        self.status = status
+        self.hip_error = hip_error
+
+
+class MlqWeight(ctypes.Structure):
+    """struct mlq_weight (include/mlq.h)."""
+    _fields_ = [
+        ("base", ctypes.c_void_p),
+        ("type", ctypes.c_int32),
+        ("n", ctypes.c_int32),
+        ("k", ctypes.c_int32),
+        ("nb", ctypes.c_int32),
+        ("qs_off", ctypes.c_uint64),
+        ("d_off", ctypes.c_uint64),
+        ("m_off", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+    ]
+
+
+# Every symbol declared in include/mlq.h, with its ctypes signature.
+_P, _I, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+_WP = ctypes.POINTER(MlqWeight)
+SIGNATURES = {
+    "mlq_status_string": ([_I], ctypes.c_char_p),
+    "mlq_last_hip_error": ([], _I),
+    "mlq_device_count": ([ctypes.POINTER(_I)], _I),
+    "mlq_block_bytes": ([_I], _Z),
+    "mlq_weight_layout": ([_I, _I, _I, _WP], _I),
+    "mlq_repack_host": ([_I, _P, _Z, _I, _I, _P, _Z], _I),
+    "mlq_repack_device": ([_I, _P, _Z, _I, _I, _P, _Z, _P], _I),
+    "mlq_dequantize": ([_WP, _I, _I, _P, _P], _I),
+    "mlq_linear": ([_WP, _P, _P, _I, _P], _I),
+    "mlq_linear_aos": ([_I, _P, _Z, _I, _I, _P, _P, _I, _P, _Z, _P], _I),
+    "mlq_linear_path": ([_WP, _P, _P, _I, _I, _P], _I),
+    "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
+}
+
+_LIB = None
+
+
+def build(quiet: bool = True) -> None:
+    """Compile libmlq.so, libmini_llama_hip.so and the C++ test binary for
+    gfx950 in place (always recompiles what changed)."""
+    cmd = ["make", "-C", HERE, "-j8"]
+    subprocess.run(cmd, check=True,
+                   stdout=subprocess.DEVNULL if quiet else None)
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded C ABI library. Raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it first (python -c "
+                "'import __graft_entry__ as g; g.build()'). There is no CPU "
+                "fallback for the HIP path.")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = res
+        _LIB = handle
+    return _LIB
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        raise MLQError(status, what, lib().mlq_last_hip_error())
+
+
+def device_count() -> int:
+    c = ctypes.c_int(0)
+    lib().mlq_device_count(ctypes.byref(c))
+    return c.value
+
+
+def weight_layout(qtype: str, n: int, k: int) -> MlqWeight:
+    w = MlqWeight()
+    _check(lib().mlq_weight_layout(TYPES[qtype], n, k, ctypes.byref(w)),
+           "mlq_weight_layout")
+    return w
+
+
+def repack_host(qtype: str, blocks: np.ndarray, n: int, k: int):
+    """GGUF AoS blocks (numpy structured or raw bytes) -> (tiled image as a
+    uint8 numpy array, MlqWeight layout with base unset)."""
+    raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+    bb = BLOCK_BYTES[qtype]
+    if raw.size % bb:
+        raise ValueError("block buffer is not a whole number of blocks")
+    w = weight_layout(qtype, n, k)
+    out = np.empty(w.bytes, np.uint8)
+    _check(lib().mlq_repack_host(TYPES[qtype], raw.ctypes.data, raw.size // bb,
+                                 n, k, out.ctypes.data, out.size),
+           "mlq_repack_host")
+    return out, w
+
+
+def _stream(stream=None) -> int:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+class TiledWeight:
+    """A weight repacked into the tiled layout, resident in device memory
+    (the analogue of HipUploadedWeight)."""
+
+    def __init__(self, qtype: str, n: int, k: int, buffer, layout: MlqWeight):
+        self.qtype, self.n, self.k = qtype, n, k
+        self.buffer = buffer  # torch uint8 device tensor owning the memory
+        self.layout = layout
+        self.layout.base = buffer.data_ptr()
+
+    @property
+    def nbytes(self) -> int:
+        return int(self.layout.bytes)
+
+    @property
+    def gguf_bytes(self) -> int:
+        """Size of the same weight as GGUF blocks (the algorithmic bytes)."""
+        return self.n * ((self.k + 31) // 32) * BLOCK_BYTES[self.qtype]
+
+
+def upload(qtype: str, blocks: np.ndarray, n: int, k: int,
+           device: str = "cuda") -> TiledWeight:
+    """Host repack + one host-to-device copy (the upload path)."""
+    import torch
+    image, layout = repack_host(qtype, blocks, n, k)
+    buf = torch.from_numpy(image).to(device)
+    return TiledWeight(qtype, n, k, buf, layout)
+
+
+def upload_aos(blocks: np.ndarray, device: str = "cuda"):
+    """Raw GGUF blocks to device memory unchanged (what the reference uploads)."""
+    import torch
+    raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+    return torch.from_numpy(raw.copy()).to(device)
+
+
+def repack_device(qtype: str, aos_dev, n: int, k: int, stream=None) -> TiledWeight:
+    """Repack GGUF blocks already in device memory with the device kernel."""
+    import torch
+    layout = weight_layout(qtype, n, k)
+    buf = torch.empty(int(layout.bytes), dtype=torch.uint8, device=aos_dev.device)
+    bb = BLOCK_BYTES[qtype]
+    _check(lib().mlq_repack_device(TYPES[qtype], aos_dev.data_ptr(),
+                                   aos_dev.numel() // bb, n, k, buf.data_ptr(),
+                                   buf.numel(), _stream(stream)),
+           "mlq_repack_device")
+    return TiledWeight(qtype, n, k, buf, layout)
+
+
+def dequantize(w: TiledWeight, row0: int = 0, rows: int | None = None,
+               stream=None):
+    """fp32 [rows, k] dequantized values (exact d*q / d*(q-8) / d*q+m)."""
+    import torch
+    rows = w.n - row0 if rows is None else rows
+    out = torch.empty((rows, w.k), dtype=torch.float32, device=w.buffer.device)
+    _check(lib().mlq_dequantize(ctypes.byref(w.layout), row0, rows,
+                                out.data_ptr(), _stream(stream)),
+           "mlq_dequantize")
+    return out
+
+
+def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None):
+    """y[m, n] = x[m, k] @ W^T on the device (x fp32 contiguous, 1-D or 2-D)."""
+    import torch
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float32 device tensor")
+    m = 1 if x.dim() == 1 else x.shape[0]
+    kx = x.shape[-1]
+    if kx != w.k:
+        raise ValueError(f"in_features mismatch: x has {kx}, weight has {w.k}")
+    if y is None:
+        shape = (w.n,) if x.dim() == 1 else (m, w.n)
+        y = torch.empty(shape, dtype=torch.float32, device=x.device)
+    _check(lib().mlq_linear_path(ctypes.byref(w.layout), x.data_ptr(),
+                                 y.data_ptr(), m, path, _stream(stream)),
+           "mlq_linear")
+    return y
+
+
+def linear_aos(qtype: str, aos_dev, n: int, k: int, x, workspace=None,
+               stream=None):
+    """Linear on raw GGUF blocks in device memory (repacked into workspace)."""
+    import torch
+    m = 1 if x.dim() == 1 else x.shape[0]
+    layout = weight_layout(qtype, n, k)
+    if workspace is None:
+        workspace = torch.empty(int(layout.bytes), dtype=torch.uint8,
+                                device=x.device)
+    y = torch.empty((n,) if x.dim() == 1 else (m, n), dtype=torch.float32,
+                    device=x.device)
+    bb = BLOCK_BYTES[qtype]
+    _check(lib().mlq_linear_aos(TYPES[qtype], aos_dev.data_ptr(),
+                                aos_dev.numel() // bb, n, k, x.data_ptr(),
+                                y.data_ptr(), m, workspace.data_ptr(),
+                                workspace.numel(), _stream(stream)),
+           "mlq_linear_aos")
+    return y
+
+
+def add_bias(y, bias, stream=None):
+    m = 1 if y.dim() == 1 else y.shape[0]
+    _check(lib().mlq_add_bias(y.data_ptr(), bias.data_ptr(), m, y.shape[-1],
+                              _stream(stream)), "mlq_add_bias")
+    return y

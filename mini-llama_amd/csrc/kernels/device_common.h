@@ -1,0 +1,69 @@
+// Device helpers shared by the gfx950 kernels.
+//
+// Weight decode without integer->float converts: a 4-bit (or biased 8-bit)
+// code c placed in the mantissa of an fp16 whose exponent gives a unit ulp
+// is the exact value bias + c:
+//   0x6400 | c        = 1024 + c   (c in bits 0..9, ulp 1 at 1024)
+//   0x5400 | (c << 4) = 64 + c     (c in bits 4..7, ulp 1/16 at 64)
+// so one AND-OR turns two codes of a 32-bit word into an fp16 pair. The bias
+// is removed either exactly in fp16 (pre-scaled MFMA operands) or once per
+// block from a precomputed sum over the activations (GEMV dot2 path).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlq {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ h2_t as_h2(uint32_t v) {
+  return __builtin_bit_cast(h2_t, v);
+}
+__device__ __forceinline__ uint32_t as_u32(h2_t v) {
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// fp32 += a.x*b.x + a.y*b.y (v_dot2c_f32_f16: fp16 products are exact in
+// fp32).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
+  return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+// q4 word -> four fp16 pairs (elements 0-1, 2-3, 4-5, 6-7 of the word's 8),
+// biased by 1024 (pairs 0, 2) and 64 (pairs 1, 3).
+struct Q4Pairs {
+  uint32_t p0, p1, p2, p3;
+};
+__device__ __forceinline__ Q4Pairs q4_pairs(uint32_t v) {
+  const uint32_t s = v >> 8;
+  Q4Pairs p;
+  p.p0 = (v & 0x000F000Fu) | 0x64006400u;
+  p.p1 = (v & 0x00F000F0u) | 0x54005400u;
+  p.p2 = (s & 0x000F000Fu) | 0x64006400u;
+  p.p3 = (s & 0x00F000F0u) | 0x54005400u;
+  return p;
+}
+
+// q8 word (codes q+128) -> two fp16 pairs (elements 0-1, 2-3), biased by
+// 1024 + 128 relative to q.
+__device__ __forceinline__ void q8_pairs(uint32_t v, uint32_t& p0, uint32_t& p1) {
+  p0 = (v & 0x00FF00FFu) | 0x64006400u;
+  p1 = ((v >> 8) & 0x00FF00FFu) | 0x64006400u;
+}
+
+// Two fp32 -> packed fp16 pair (round to nearest even).
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  h2_t h;
+  h.x = (_Float16)a;
+  h.y = (_Float16)b;
+  return as_u32(h);
+}
+
+}  // namespace mlq

@@ -1,0 +1,148 @@
+// Weight-format kernels for gfx950:
+//  - repack_kernel: GGUF AoS blocks (device) -> tiled layout (mlq_layout.h);
+//    the device twin of the host repack used by the upload path.
+//  - dequant_kernel: tiled layout -> fp32 rows, exactly d*q / d*(q-8) /
+//    d*q+m, the reference's dequantizeFromQ* (src/quant.cc:192-392).
+//  - bias_kernel: y[m, :] += bias (the reference adds it on the host,
+//    src/cuda_quant.cu:229-235).
+// These are off the hot path (one-time or debug); they favour clarity.
+#include <hip/hip_runtime.h>
+
+#include "../mlq_layout.h"
+#include "device_common.h"
+#include "launch.h"
+
+namespace mlq {
+namespace {
+
+struct RepackArgs {
+  const uint8_t* aos;  // GGUF blocks, row-major [n][nb]
+  uint8_t* qs;
+  uint16_t* d;
+  uint16_t* m;
+  Geometry geo;
+};
+
+// One thread per padded (row, block); padding blocks decode to 0.
+template <int QT>
+__global__ void repack_kernel(RepackArgs a) {
+  const int bpr = a.geo.g * kGroupBlocks;  // padded blocks per row
+  const uint64_t total = (uint64_t)a.geo.nt * kTileRows * bpr;
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int row = (int)(idx / bpr), b = (int)(idx % bpr);
+  const bool real = row < a.geo.n && b < a.geo.nb;
+  const int bytes = QT == MLQ_Q8_0 ? 34 : (QT == MLQ_Q4_0 ? 18 : 20);
+  const uint8_t* src =
+      real ? a.aos + ((uint64_t)row * a.geo.nb + b) * bytes : nullptr;
+  repack_block(QT, a.geo, row, b, src, a.qs, a.d, a.m);
+}
+
+struct DequantArgs {
+  const uint8_t* qs;
+  const uint16_t* d;
+  const uint16_t* m;
+  float* out;
+  Geometry geo;
+  int row0, rows;
+};
+
+// One thread per output element of rows [row0, row0 + rows): exactly the
+// reference's d*q, d*(q-8), d*q+m in fp32 (d*q is exact, so contraction of
+// the q4_1 multiply-add cannot change the result).
+template <int QT>
+__global__ void dequant_kernel(DequantArgs a) {
+  const int k = a.geo.k;
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (uint64_t)a.rows * k) return;
+  const int row = a.row0 + (int)(idx / k);
+  const int kk = (int)(idx % k);
+  const int b = kk / kQK, e = kk % kQK;
+  const uint64_t si = scale_index(a.geo, row, b);
+  const float d = half_bits_to_float(a.d[si]);
+  const int c = read_code(QT, a.geo, a.qs, row, b, e);
+  float v;
+  if (QT == MLQ_Q8_0) {
+    v = d * (float)c;
+  } else if (QT == MLQ_Q4_0) {
+    v = d * (float)(c - 8);
+  } else {
+    v = d * (float)c + half_bits_to_float(a.m[si]);
+  }
+  a.out[idx] = v;
+}
+
+__global__ void bias_kernel(float* y, const float* bias, int m, int n) {
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (uint64_t)m * n) return;
+  y[idx] += bias[idx % n];
+}
+
+}  // namespace
+
+hipError_t launch_repack(int type, const void* aos, int n, int k,
+                         const mlq_weight& w, hipStream_t stream) {
+  const Geometry geo = geometry(n, k);
+  RepackArgs a;
+  a.aos = (const uint8_t*)aos;
+  a.qs = (uint8_t*)w.base + w.qs_off;
+  a.d = (uint16_t*)((uint8_t*)w.base + w.d_off);
+  a.m = type == MLQ_Q4_1 ? (uint16_t*)((uint8_t*)w.base + w.m_off) : nullptr;
+  a.geo = geo;
+  const uint64_t total = (uint64_t)geo.nt * kTileRows * geo.g * kGroupBlocks;
+  const unsigned threads = 256;
+  const unsigned blocks = (unsigned)((total + threads - 1) / threads);
+  switch (type) {
+    case MLQ_Q8_0:
+      repack_kernel<MLQ_Q8_0><<<blocks, threads, 0, stream>>>(a);
+      break;
+    case MLQ_Q4_0:
+      repack_kernel<MLQ_Q4_0><<<blocks, threads, 0, stream>>>(a);
+      break;
+    default:
+      repack_kernel<MLQ_Q4_1><<<blocks, threads, 0, stream>>>(a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant(const mlq_weight& w, int row0, int rows, float* out,
+                          hipStream_t stream) {
+  const Geometry geo = geometry(w.n, w.k);
+  DequantArgs a;
+  a.qs = (const uint8_t*)w.base + w.qs_off;
+  a.d = (const uint16_t*)((const uint8_t*)w.base + w.d_off);
+  a.m = w.type == MLQ_Q4_1
+            ? (const uint16_t*)((const uint8_t*)w.base + w.m_off)
+            : nullptr;
+  a.out = out;
+  a.geo = geo;
+  a.row0 = row0;
+  a.rows = rows;
+  const uint64_t total = (uint64_t)rows * w.k;
+  const unsigned threads = 256;
+  const unsigned blocks = (unsigned)((total + threads - 1) / threads);
+  switch (w.type) {
+    case MLQ_Q8_0:
+      dequant_kernel<MLQ_Q8_0><<<blocks, threads, 0, stream>>>(a);
+      break;
+    case MLQ_Q4_0:
+      dequant_kernel<MLQ_Q4_0><<<blocks, threads, 0, stream>>>(a);
+      break;
+    default:
+      dequant_kernel<MLQ_Q4_1><<<blocks, threads, 0, stream>>>(a);
+      break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_bias(float* y, const float* bias, int m, int n,
+                       hipStream_t stream) {
+  const uint64_t total = (uint64_t)m * n;
+  const unsigned threads = 256;
+  const unsigned blocks = (unsigned)((total + threads - 1) / threads);
+  bias_kernel<<<blocks, threads, 0, stream>>>(y, bias, m, n);
+  return hipGetLastError();
+}
+
+}  // namespace mlq

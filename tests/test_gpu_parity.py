@@ -1,0 +1,267 @@
+"""GPU parity of the HIP quantized-Linear path against the CPU oracle.
+
+Everything here calls libmlq through its C ABI (ctypes); the oracle
+(restated reference CPU path, src/quant.cc:192-650) is the checker.
+  - dequantization: bit-exact (integer/byte work and exact d*q products);
+  - Linear outputs: the stated tolerance (tests/conftest.py), plus the
+    reference CUDA tests' 1e-4 absolute bound on their own inputs;
+  - full benchmark shapes: oracle on sampled output rows.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import error_report, make_blocks, make_x, tolerance_ok
+
+pytestmark = pytest.mark.gpu
+
+TYPES = ["q8_0", "q4_0", "q4_1"]
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _dev(a, cuda):
+    return _torch().from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+def _print_case(**kw):
+    print("case:", " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+# --------------------------------------------------------------------------
+# dequantization: bit-exact
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("n,k", [(1, 32), (16, 128), (17, 100), (40, 1000),
+                                 (33, 4096)])
+def test_dequant_bit_exact(pkg, oracle, cuda, qtype, n, k):
+    _print_case(test="dequant", qtype=qtype, n=n, k=k)
+    blocks = make_blocks(qtype, n, k, seed=11 * n + k)
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    got = pkg.dequantize(tw).cpu().numpy()
+    ref = oracle.dequantize(blocks, (n, k), qtype)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_dequant_subnormal_and_special_scales(pkg, oracle, cuda, qtype):
+    """Every fp16 scale class: subnormals, zero, negative zero, max normal."""
+    n, k = 64, 256
+    blocks = make_blocks(qtype, n, k, seed=5)
+    specials = np.array([0x0001, 0x03ff, 0x0200, 0x0000, 0x8000, 0x8001,
+                         0x7bff, 0x0400, 0x3c00, 0xbc00], np.uint16)
+    blocks["d"][: specials.size * 10] = np.repeat(specials, 10)
+    if qtype == "q4_1":
+        blocks["m"][::7] = 0x8123  # negative subnormal mins
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    got = pkg.dequantize(tw).cpu().numpy()
+    ref = oracle.dequantize(blocks, (n, k), qtype)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype,n,k", [("q8_0", 4096, 4096), ("q4_0", 18944, 3584),
+                                       ("q4_1", 4096, 14336)])
+def test_dequant_bit_exact_config_rows(pkg, oracle, cuda, qtype, n, k):
+    """Benchmark shapes: rows spread over the whole weight, incl. the last."""
+    _print_case(test="dequant_config", qtype=qtype, n=n, k=k)
+    blocks = make_blocks(qtype, n, k, seed=3)
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    nb = (k + 31) // 32
+    for row0 in (0, n // 3 + 5, n - 7):
+        got = pkg.dequantize(tw, row0, 7).cpu().numpy()
+        sub = blocks[row0 * nb:(row0 + 7) * nb]
+        ref = oracle.dequantize(sub, (7, k), qtype)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), row0
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("n,k", [(16, 128), (45, 300), (100, 4096)])
+def test_device_repack_equals_host_repack(pkg, cuda, qtype, n, k):
+    blocks = make_blocks(qtype, n, k, seed=n + k)
+    host = pkg.upload(qtype, blocks, n, k, device=cuda)
+    dev = pkg.repack_device(qtype, pkg.upload_aos(blocks, device=cuda), n, k)
+    _torch().cuda.synchronize()
+    lay = host.layout
+    h = host.buffer.cpu().numpy()
+    d = dev.buffer.cpu().numpy()
+    # compare quant, scale (and min) regions up to their real lengths (the
+    # alignment gaps between regions are never read)
+    geo_units = ((n + 15) // 16) * (((k + 31) // 32 + 3) // 4)
+    qbytes = geo_units * 64 * (32 if qtype == "q8_0" else 16)
+    sbytes = geo_units * 64 * 2
+    assert np.array_equal(h[:qbytes], d[:qbytes])
+    assert np.array_equal(h[lay.d_off:lay.d_off + sbytes], d[lay.d_off:lay.d_off + sbytes])
+    if qtype == "q4_1":
+        assert np.array_equal(h[lay.m_off:lay.m_off + sbytes],
+                              d[lay.m_off:lay.m_off + sbytes])
+
+
+# --------------------------------------------------------------------------
+# Linear: reference CUDA-test inputs at the reference's 1e-4 bound
+# --------------------------------------------------------------------------
+def _fill_linear(n, scale, offset):
+    return (offset + scale * np.arange(n, dtype=np.float32)).astype(np.float32)
+
+
+def _ref_q41_blocks(out_features, in_features):
+    """tests/test_cuda.cc:116-132 makeQ41Blocks (d = 0.5, m = 0)."""
+    import oracle as o
+    bpr = (in_features + 31) // 32
+    b = np.zeros(out_features * bpr, o.BLOCK_Q4_1)
+    b["d"] = 0x3800
+    b["m"] = 0
+    i = np.arange(16)
+    b["qs"] = (((i * 3 + 1) & 0xF) | (((i * 5 + 2) & 0xF) << 4)).astype(np.uint8)
+    return b
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("path", [1, 2])  # GEMV, MFMA GEMM
+def test_reference_cuda_test_inputs(pkg, oracle, cuda, qtype, path):
+    """tests/test_cuda.cc:679-743 inputs: W[4,32] fillLinear(0.05,-1),
+    x[32] fillLinear(0.1,-0.4), x2[2,32] fillLinear(0.07,-0.3)."""
+    w = _fill_linear(128, 0.05, -1.0).reshape(4, 32)
+    if qtype == "q4_1":
+        blocks = _ref_q41_blocks(4, 32)
+    else:
+        blocks = oracle.quantize(w, qtype)
+    x = _fill_linear(32, 0.1, -0.4)
+    x2 = _fill_linear(64, 0.07, -0.3).reshape(2, 32)
+    tw = pkg.upload(qtype, blocks, 4, 32, device=cuda)
+    for xv in (x, x2):
+        ref = oracle.linear(xv, blocks, (4, 32), qtype)
+        got = pkg.linear(tw, _dev(xv, cuda), path=path).cpu().numpy()
+        if path == 1:
+            # GEMV is fp32-class: the reference's own 1e-4 absolute bound
+            assert np.max(np.abs(got - ref)) <= 1e-4, (got, ref)
+        else:
+            assert tolerance_ok(got, ref, np.atleast_2d(xv), 32).all(), (got, ref)
+
+
+# --------------------------------------------------------------------------
+# Linear: random shapes, both kernel families, all types
+# --------------------------------------------------------------------------
+SHAPES = [(1, 16, 32), (1, 17, 33), (1, 100, 1000), (1, 300, 4096),
+          (2, 64, 256), (3, 48, 200), (4, 130, 640), (8, 64, 2048),
+          (5, 33, 4096), (16, 256, 512), (64, 128, 1024), (130, 70, 300),
+          (257, 300, 256),
+          # one-wave workgroups with m > 4 (fewer threads than m*16 outputs)
+          (5, 100, 512), (8, 40, 256), (6, 20, 100)]
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_linear_matches_oracle(pkg, oracle, cuda, qtype, m, n, k):
+    _print_case(test="linear", qtype=qtype, m=m, n=n, k=k)
+    blocks = make_blocks(qtype, n, k, seed=m * 1000 + n + k)
+    x = make_x(m, k, seed=m + 7 * k)
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    xd = _dev(x, cuda)
+    ref = oracle.linear(x, blocks, (n, k), qtype, threads=8)
+    paths = [0, 2] + ([1] if m <= 8 else [])
+    for path in paths:
+        got = pkg.linear(tw, xd, path=path).cpu().numpy()
+        ok = tolerance_ok(got, ref, x, k)
+        assert ok.all(), (path, error_report(got, ref, x, k))
+        if path == 1:
+            # decode path is fp32-class: far inside the stated tolerance
+            rep = error_report(got, ref, x, k)
+            assert rep["max_abs_over_atol"] < 0.05, rep
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_linear_1d_input_and_aos_path(pkg, oracle, cuda, qtype):
+    n, k = 80, 544
+    blocks = make_blocks(qtype, n, k, seed=21)
+    x = make_x(1, k, seed=22)[0]
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    y_tiled = pkg.linear(tw, _dev(x, cuda)).cpu().numpy()
+    assert y_tiled.shape == (n,)
+    y_aos = pkg.linear_aos(qtype, pkg.upload_aos(blocks, device=cuda), n, k,
+                           _dev(x, cuda)).cpu().numpy()
+    assert np.array_equal(y_tiled, y_aos)  # same kernels, same bits
+    ref = oracle.linear(x, blocks, (n, k), qtype)
+    assert tolerance_ok(y_tiled, ref, x[None], k).all()
+
+
+def test_bias_kernel(pkg, cuda):
+    torch = _torch()
+    y = torch.arange(12, dtype=torch.float32, device=cuda).reshape(3, 4)
+    b = torch.tensor([1.0, -2.0, 0.5, 4.0], device=cuda)
+    got = pkg.add_bias(y.clone(), b).cpu().numpy()
+    assert np.array_equal(got, np.arange(12, dtype=np.float32).reshape(3, 4) +
+                          np.array([1.0, -2.0, 0.5, 4.0], np.float32))
+
+
+def test_validation_errors(pkg, cuda):
+    torch = _torch()
+    blocks = make_blocks("q4_0", 16, 64, seed=1)
+    tw = pkg.upload("q4_0", blocks, 16, 64, device=cuda)
+    with pytest.raises(ValueError):
+        pkg.linear(tw, torch.zeros(32, device=cuda))
+    with pytest.raises(pkg.MLQError) as e:
+        pkg.linear(tw, torch.zeros((9, 64), device=cuda), path=pkg.PATH_GEMV)
+    assert e.value.status == -5
+    aos = pkg.upload_aos(blocks[:-1], device=cuda)
+    with pytest.raises(pkg.MLQError) as e:
+        pkg.linear_aos("q4_0", aos, 16, 64, torch.zeros(64, device=cuda))
+    assert e.value.status == -3
+
+
+# --------------------------------------------------------------------------
+# Full benchmark shapes (sampled oracle rows)
+# --------------------------------------------------------------------------
+CONFIGS = [("c0", "q8_0", 1, 4096, 4096), ("c1", "q4_0", 1, 18944, 3584),
+           ("c2", "q4_1", 1, 4096, 14336), ("c3", "q4_0", 4, 4096, 4096),
+           ("c3", "q4_0", 16, 4096, 4096), ("c3", "q4_0", 64, 4096, 4096),
+           ("c4", "q8_0", 512, 11008, 4096)]
+
+
+@pytest.mark.parametrize("cfg,qtype,m,n,k", CONFIGS)
+def test_config_shapes(pkg, oracle, cuda, cfg, qtype, m, n, k):
+    _print_case(test="config", cfg=cfg, qtype=qtype, m=m, n=n, k=k)
+    blocks = make_blocks(qtype, n, k, seed=1000 + n)
+    x = make_x(m, k, seed=2000 + m)
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    y = pkg.linear(tw, _dev(x, cuda)).cpu().numpy()
+    assert np.isfinite(y).all()
+    rng = np.random.default_rng(m + n)
+    rows = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, 64)]))
+    nb = (k + 31) // 32
+    ms = np.arange(m) if m <= 8 else np.unique(
+        np.concatenate([[0, m - 1], rng.integers(0, m, 6)]))
+    xs = x[ms]
+    for r in rows:
+        ref = oracle.linear(xs, blocks[r * nb:(r + 1) * nb], (1, k), qtype)
+        got = y[ms][:, [r]]
+        assert tolerance_ok(got, ref, xs, k).all(), (r, error_report(got, ref, xs, k))
+
+
+def test_linearity_full_c1(pkg, cuda):
+    """Size-independent property at the headline shape: W(ax+by) = aWx + bWy."""
+    torch = _torch()
+    n, k = 18944, 3584
+    blocks = make_blocks("q4_0", n, k, seed=77)
+    tw = pkg.upload("q4_0", blocks, n, k, device=cuda)
+    x = _dev(make_x(1, k, seed=1)[0], cuda)
+    z = _dev(make_x(1, k, seed=2)[0], cuda)
+    a, b = 0.5, -2.0  # powers of two keep the combination exact
+    y = pkg.linear(tw, a * x + b * z)
+    y2 = a * pkg.linear(tw, x) + b * pkg.linear(tw, z)
+    scale = torch.linalg.vector_norm(x) * np.sqrt(k / 4096) * 1e-3
+    assert torch.max(torch.abs(y - y2)).item() <= 4 * scale.item()
+
+
+def test_cpp_interface_tests(pkg):
+    """The C++ host-interface tests (tests/cpp/test_hip_quant.cc)."""
+    import subprocess
+    r = subprocess.run([pkg.CPP_TEST_PATH], capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout[-4000:])
+    print(r.stderr[-4000:])
+    assert r.returncode == 0
+    assert "(skip" not in r.stdout
