@@ -149,6 +149,13 @@ enum mlq_path { MLQ_PATH_AUTO = 0, MLQ_PATH_GEMV = 1, MLQ_PATH_MFMA = 2 };
 int mlq_linear_path(const mlq_weight* w, const float* x, float* y, int m,
                     int path, mlq_stream_t stream);
 
+/* GEMV work decomposition override for tuning and tests (process-wide):
+ * split = waves per 16-row tile (1, 2, 4, 8 or 16; 0 = automatic),
+ * depth = 128-k groups each wave loads ahead (2, 4 or 8; 0 = automatic).
+ * The planner still widens the split when the activation staging would not
+ * fit in LDS. Returns MLQ_ERR_INVALID_ARG for other values. */
+int mlq_set_gemv_plan(int split, int depth);
+
 /* Add bias[n] to every row of y[m, n] on the device (the reference adds the
  * bias on the host after download, src/cuda_quant.cu:229-235, 327-329). */
 int mlq_add_bias(float* y, const float* bias, int m, int n,

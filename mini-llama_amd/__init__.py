@@ -77,6 +77,7 @@ SIGNATURES = {
     "mlq_linear_aos": ([_I, _P, _Z, _I, _I, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_linear_path": ([_WP, _P, _P, _I, _I, _P], _I),
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
+    "mlq_set_gemv_plan": ([_I, _I], _I),
 }
 
 _LIB = None
@@ -244,6 +245,11 @@ def linear_aos(qtype: str, aos_dev, n: int, k: int, x, workspace=None,
                                 workspace.numel(), _stream(stream)),
            "mlq_linear_aos")
     return y
+
+
+def set_gemv_plan(split: int = 0, depth: int = 0) -> None:
+    """Override the GEMV decomposition (0 = automatic) for tuning/tests."""
+    _check(lib().mlq_set_gemv_plan(split, depth), "mlq_set_gemv_plan")
 
 
 def add_bias(y, bias, stream=None):

@@ -212,6 +212,15 @@ int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,
   return mlq_linear(&w, x, y, m, stream);
 }
 
+int mlq_set_gemv_plan(int split, int depth) {
+  const bool split_ok = split == 0 || split == 1 || split == 2 || split == 4 ||
+                        split == 8 || split == 16;
+  const bool depth_ok = depth == 0 || depth == 2 || depth == 4 || depth == 8;
+  if (!split_ok || !depth_ok) return MLQ_ERR_INVALID_ARG;
+  set_gemv_plan(split, depth);
+  return MLQ_OK;
+}
+
 int mlq_add_bias(float* y, const float* bias, int m, int n,
                  mlq_stream_t stream) {
   if (y == nullptr || bias == nullptr) return MLQ_ERR_INVALID_ARG;

@@ -17,6 +17,7 @@ namespace mlq {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ h2_t as_h2(uint32_t v) {
@@ -36,6 +37,19 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t bits) {
   return (float)__builtin_bit_cast(_Float16, bits);
 }
 
+// (v & mask) | bits in one VALU op: gfx950's three-input v_bitop3_b32 with
+// truth table (a & b) | c. Left to itself the compiler emits a separate AND
+// and OR (VOP3 takes no literals and one scalar operand); through the
+// builtin the mask sits in an SGPR and the OR constant in a hoisted VGPR, and
+// the instruction stays visible to the compiler's hazard tracking (an
+// inline-asm version is not: it can overwrite MFMA source registers that are
+// still being read).
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask,
+                                           uint32_t bits) {
+  constexpr unsigned kAndOr = (0xF0 & 0xCC) | 0xAA;  // f(a, b, c) = (a & b) | c
+  return __builtin_amdgcn_bitop3_b32(v, mask, bits, kAndOr);
+}
+
 // q4 word -> four fp16 pairs (elements 0-1, 2-3, 4-5, 6-7 of the word's 8),
 // biased by 1024 (pairs 0, 2) and 64 (pairs 1, 3).
 struct Q4Pairs {
@@ -44,18 +58,18 @@ struct Q4Pairs {
 __device__ __forceinline__ Q4Pairs q4_pairs(uint32_t v) {
   const uint32_t s = v >> 8;
   Q4Pairs p;
-  p.p0 = (v & 0x000F000Fu) | 0x64006400u;
-  p.p1 = (v & 0x00F000F0u) | 0x54005400u;
-  p.p2 = (s & 0x000F000Fu) | 0x64006400u;
-  p.p3 = (s & 0x00F000F0u) | 0x54005400u;
+  p.p0 = and_or(v, 0x000F000Fu, 0x64006400u);
+  p.p1 = and_or(v, 0x00F000F0u, 0x54005400u);
+  p.p2 = and_or(s, 0x000F000Fu, 0x64006400u);
+  p.p3 = and_or(s, 0x00F000F0u, 0x54005400u);
   return p;
 }
 
 // q8 word (codes q+128) -> two fp16 pairs (elements 0-1, 2-3), biased by
 // 1024 + 128 relative to q.
 __device__ __forceinline__ void q8_pairs(uint32_t v, uint32_t& p0, uint32_t& p1) {
-  p0 = (v & 0x00FF00FFu) | 0x64006400u;
-  p1 = ((v >> 8) & 0x00FF00FFu) | 0x64006400u;
+  p0 = and_or(v, 0x00FF00FFu, 0x64006400u);
+  p1 = and_or(v >> 8, 0x00FF00FFu, 0x64006400u);
 }
 
 // Two fp32 -> packed fp16 pair (round to nearest even).

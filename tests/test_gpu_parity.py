@@ -174,6 +174,27 @@ def test_linear_matches_oracle(pkg, oracle, cuda, qtype, m, n, k):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("split", [0, 1, 2, 4, 8, 16])
+@pytest.mark.parametrize("depth", [2, 4, 8])
+def test_gemv_every_plan(pkg, oracle, cuda, qtype, split, depth):
+    """Every GEMV decomposition (K split x load depth) on shapes whose runs
+    exceed the depth (exercising the refill ring) and have ragged tails."""
+    _print_case(test="gemv_plan", qtype=qtype, split=split, depth=depth)
+    pkg.set_gemv_plan(split, depth)
+    try:
+        for m, n, k in [(1, 48, 4000), (3, 40, 2100), (8, 17, 1500)]:
+            blocks = make_blocks(qtype, n, k, seed=n + k + m)
+            x = make_x(m, k, seed=k + 3)
+            tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+            got = pkg.linear(tw, _dev(x, cuda), path=pkg.PATH_GEMV).cpu().numpy()
+            ref = oracle.linear(x, blocks, (n, k), qtype, threads=8)
+            rep = error_report(got, ref, x, k)
+            assert np.isfinite(got).all() and rep["max_abs_over_atol"] < 0.05, (m, n, k, rep)
+    finally:
+        pkg.set_gemv_plan(0, 0)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
 def test_linear_1d_input_and_aos_path(pkg, oracle, cuda, qtype):
     n, k = 80, 544
     blocks = make_blocks(qtype, n, k, seed=21)
