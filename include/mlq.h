@@ -150,11 +150,12 @@ int mlq_linear_path(const mlq_weight* w, const float* x, float* y, int m,
                     int path, mlq_stream_t stream);
 
 /* GEMV work decomposition override for tuning and tests (process-wide):
- * split = waves per 16-row tile (1, 2, 4, 8 or 16; 0 = automatic),
- * depth = 128-k groups each wave loads ahead (2, 4 or 8; 0 = automatic).
- * The planner still widens the split when the activation staging would not
- * fit in LDS. Returns MLQ_ERR_INVALID_ARG for other values. */
-int mlq_set_gemv_plan(int split, int depth);
+ * split = waves (K slices) per 16-row tile: 1, 2, 4, 8 or 16; 0 restores
+ * the automatic choice. The planner still widens the split when the
+ * activation staging would not fit in LDS. How many groups a wave keeps in
+ * flight follows from the slice length. Returns MLQ_ERR_INVALID_ARG for
+ * other values. */
+int mlq_set_gemv_split(int split);
 
 /* Add bias[n] to every row of y[m, n] on the device (the reference adds the
  * bias on the host after download, src/cuda_quant.cu:229-235, 327-329). */

@@ -77,7 +77,7 @@ SIGNATURES = {
     "mlq_linear_aos": ([_I, _P, _Z, _I, _I, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_linear_path": ([_WP, _P, _P, _I, _I, _P], _I),
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
-    "mlq_set_gemv_plan": ([_I, _I], _I),
+    "mlq_set_gemv_split": ([_I], _I),
 }
 
 _LIB = None
@@ -247,9 +247,9 @@ def linear_aos(qtype: str, aos_dev, n: int, k: int, x, workspace=None,
     return y
 
 
-def set_gemv_plan(split: int = 0, depth: int = 0) -> None:
-    """Override the GEMV decomposition (0 = automatic) for tuning/tests."""
-    _check(lib().mlq_set_gemv_plan(split, depth), "mlq_set_gemv_plan")
+def set_gemv_split(split: int = 0) -> None:
+    """Override the GEMV K split (waves per tile; 0 = automatic)."""
+    _check(lib().mlq_set_gemv_split(split), "mlq_set_gemv_split")
 
 
 def add_bias(y, bias, stream=None):

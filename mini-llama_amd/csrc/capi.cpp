@@ -212,12 +212,11 @@ int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,
   return mlq_linear(&w, x, y, m, stream);
 }
 
-int mlq_set_gemv_plan(int split, int depth) {
+int mlq_set_gemv_split(int split) {
   const bool split_ok = split == 0 || split == 1 || split == 2 || split == 4 ||
                         split == 8 || split == 16;
-  const bool depth_ok = depth == 0 || depth == 2 || depth == 4 || depth == 8;
-  if (!split_ok || !depth_ok) return MLQ_ERR_INVALID_ARG;
-  set_gemv_plan(split, depth);
+  if (!split_ok) return MLQ_ERR_INVALID_ARG;
+  set_gemv_split(split);
   return MLQ_OK;
 }
 

@@ -72,6 +72,35 @@ __device__ __forceinline__ void q8_pairs(uint32_t v, uint32_t& p0, uint32_t& p1)
   p1 = and_or(v >> 8, 0x00FF00FFu, 0x64006400u);
 }
 
+// Buffer resources: a scalar base address plus a byte range. A load whose
+// offset lies past the range returns zeros without touching memory, which
+// lets kernels read ragged tails (and skip whole groups) with no branches.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw (untyped, stride 0) buffer: word 3 selects 32-bit dword data.
+constexpr int kRawBufferFlags = 0x00020000;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)bytes, kRawBufferFlags);
+}
+__device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t voff,
+                                            uint32_t soff) {
+  return __builtin_bit_cast(
+      uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ uint2 buf_load8(rsrc_t r, uint32_t voff,
+                                           uint32_t soff) {
+  return __builtin_bit_cast(
+      uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(rsrc_t r, uint32_t voff,
+                                              uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+
 // Two fp32 -> packed fp16 pair (round to nearest even).
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   h2_t h;

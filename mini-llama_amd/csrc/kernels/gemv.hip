@@ -2,26 +2,36 @@
 // m = 1..8 activation rows.
 //
 // Replaces q80LinearKernel / q40LinearKernel / q41LinearKernel
-// (src/cuda_quant.cu:78-182) for decode-sized m. Design (HBM-bound):
+// (src/cuda_quant.cu:78-182) for decode-sized m. The kernel is held to the
+// HBM roofline, so its structure follows where the bytes and the VALU issue
+// slots go:
 //  - A workgroup owns one 16-row tile; its S waves (S = 1..16) split the
-//    tile's K range into contiguous runs of 128-k groups, sized so that the
-//    whole grid is resident at once (about 16 waves per CU). Per group a
+//    tile's K range into contiguous slices of `gw` 128-k groups. Per group a
 //    wave reads one contiguous 1 KiB (q4) / 2 KiB (q8) line with a dwordx4
 //    per lane plus an 8-byte scale load; every weight byte is read from HBM
-//    exactly once. Up to D groups are loaded up front (a register ring for
-//    longer runs), and each group is decoded as soon as its data lands.
+//    exactly once.
+//  - All loads go through buffer resources built per wave (scalar base +
+//    byte range), so addresses are one VGPR offset per lane plus a scalar
+//    offset per group, and anything past the wave's range (ragged K tails,
+//    the groups of a shorter last slice) reads as zero with no branches.
+//  - Order of issue: the wave's activation slice first, then the weight
+//    lines of all its groups (GW = groups per wave, a compile-time 1..8),
+//    then the fp32 -> fp16 hi/lo conversion of the activations into the
+//    wave's private LDS slice, which therefore overlaps the weight fetch.
+//    The group loop has no data-dependent branch: a shorter last slice
+//    processes zero groups (zero scales, zero activations). Slices longer
+//    than 8 groups run a ring of 8 slots instead, each refilled 8 groups
+//    ahead as soon as its codes are decoded (refills past the slice read
+//    zeros, so they need no branch either).
 //  - Lane L = n + 16*kq holds quarter kq of the group's 4 blocks of row n,
 //    which is the B operand of v_mfma_f32_16x16x32_f16 for one block. Codes
 //    are decoded EXACTLY to fp16 (q-8, q, or q): one AND-OR places a code in
 //    the mantissa of 1024 (or 64), one packed fp16 subtract removes the bias.
-//  - Each wave stages the activations of its own K range in a private LDS
-//    slice as an fp16 hi/lo pair (x = hi + lo to ~2^-22); the activation
-//    loads are issued before the weight loads, so staging never waits on
-//    HBM and no workgroup barrier is needed before the math. MFMA row 2r is
-//    hi, row 2r+1 is lo of activation row r: up to 8 rows in one MFMA.
-//  - Per block: acc += d * (D[hi] + D[lo]) in fp32 (+ m * sum(x) for q4_1),
-//    so the result is fp32-class accurate (products are exact in fp32).
-//  - K-split waves combine partial sums through LDS in a fixed order.
+//  - MFMA row 2r is the fp16 hi part, row 2r+1 the lo part of activation row
+//    r (x = hi + lo to ~2^-22): up to 8 rows in one MFMA. Per block:
+//    acc += d * (D[hi] + D[lo]) in fp32 (+ m * sum(x) for q4_1). Products
+//    are exact in fp32, so the result is fp32-class accurate.
+//  - K slices combine through LDS in slice order (deterministic).
 // Activations must be finite and |x| < 65504 (the fp16 range of the hi part).
 #include <hip/hip_runtime.h>
 
@@ -38,7 +48,8 @@ namespace {
 constexpr int kMaxSplit = 16;       // waves per workgroup (one tile)
 constexpr int kTargetWaves = 4096;  // ~16 resident waves per CU on 256 CUs
 constexpr int kRowPadHalves = 32;   // 64 B: consecutive LDS rows hit other banks
-constexpr int kMaxXRegs = 4;        // float4 activation loads held per lane
+constexpr int kUnitScaleBytes = kTileRows * kGroupBlocks * 2;  // 128 B
+constexpr int kXRegs = 4;           // float4 activation loads held per lane
 
 // Largest dynamic LDS allocation a workgroup may use on the current device
 // (160 KiB on gfx950), read once.
@@ -57,16 +68,21 @@ size_t lds_limit() {
 
 struct GemvArgs {
   const uint8_t* qs;
-  const uint16_t* d;
-  const uint16_t* mn;
+  const uint8_t* d;
+  const uint8_t* mn;
   const float* x;
   float* y;
   int m, n, k, g, nt;
   int split;     // waves per workgroup = K slices of its tile
-  int gw;        // groups per wave (last slice may be shorter)
+  int gw;        // groups per wave (the last slice may be shorter)
   int xstride;   // fp16 elements per staged activation row
   int wave_lds;  // bytes of LDS per wave (activation slice + block sums)
 };
+
+template <int QT>
+constexpr uint32_t unit_quant_bytes() {
+  return QT == MLQ_Q8_0 ? 2048u : 1024u;
+}
 
 template <int QT>
 struct Slot {
@@ -76,19 +92,19 @@ struct Slot {
   uint2 m;   // four fp16 mins (q4_1)
 };
 
+struct WaveRsrc {
+  rsrc_t q, d, m;
+};
+
+// Loads group j of the wave's slice (zeros when j is past the slice).
 template <int QT>
-__device__ __forceinline__ void load_slot(const GemvArgs& a, Slot<QT>& s,
-                                          size_t unit, int lane) {
-  const int n = lane & 15;
-  if (QT == MLQ_Q8_0) {
-    s.q = *(const uint4*)(a.qs + ((unit * 2) * kLanes + lane) * 16);
-    s.q2 = *(const uint4*)(a.qs + ((unit * 2 + 1) * kLanes + lane) * 16);
-  } else {
-    s.q = *(const uint4*)(a.qs + (unit * kLanes + lane) * 16);
-  }
-  s.d = *(const uint2*)(a.d + (unit * kTileRows + n) * kGroupBlocks);
-  if (QT == MLQ_Q4_1)
-    s.m = *(const uint2*)(a.mn + (unit * kTileRows + n) * kGroupBlocks);
+__device__ __forceinline__ void load_group(const WaveRsrc& r, Slot<QT>& s,
+                                           int j, uint32_t qoff, uint32_t soff) {
+  const uint32_t qb = (uint32_t)j * unit_quant_bytes<QT>();
+  s.q = buf_load16(r.q, qoff, qb);
+  if (QT == MLQ_Q8_0) s.q2 = buf_load16(r.q, qoff, qb + 1024u);
+  s.d = buf_load8(r.d, soff, (uint32_t)j * kUnitScaleBytes);
+  if (QT == MLQ_Q4_1) s.m = buf_load8(r.m, soff, (uint32_t)j * kUnitScaleBytes);
 }
 
 // Exact fp16 decode of 8 codes of one quarter-block (MFMA B fragment).
@@ -118,21 +134,22 @@ __device__ __forceinline__ h8_t decode8(uint32_t w0, uint32_t w1) {
   return __builtin_bit_cast(h8_t, o);
 }
 
-__device__ __forceinline__ float scale_at(uint2 s, int j) {
+__device__ __forceinline__ _Float16 half_at(uint2 s, int j) {
   const uint32_t w = (j & 2) ? s.y : s.x;
-  return half_bits_to_float((uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu)));
+  return __builtin_bit_cast(_Float16,
+                            (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu)));
 }
 
-// Four consecutive activations x[row][k..k+3], zero past k (vec: k is a
-// multiple of 4, so whole float4 loads stay in bounds and aligned).
-__device__ __forceinline__ float4 load_x4(const float* xr, int k, int kmax,
-                                          bool vec) {
-  if (vec && k + 4 <= kmax) return *(const float4*)(xr + k);
+// Four activations x[row][4c .. 4c+3] of the slice (zeros past the range).
+// vec: the range is a whole number of float4 (k % 4 == 0); otherwise every
+// element is range-checked on its own.
+__device__ __forceinline__ float4 load_x4(rsrc_t r, int c, bool vec) {
+  if (vec) return __builtin_bit_cast(float4, buf_load16(r, (uint32_t)c * 16u, 0));
   float4 v;
-  v.x = k + 0 < kmax ? xr[k + 0] : 0.0f;
-  v.y = k + 1 < kmax ? xr[k + 1] : 0.0f;
-  v.z = k + 2 < kmax ? xr[k + 2] : 0.0f;
-  v.w = k + 3 < kmax ? xr[k + 3] : 0.0f;
+  v.x = __builtin_bit_cast(float, buf_load4(r, (uint32_t)c * 16u, 0));
+  v.y = __builtin_bit_cast(float, buf_load4(r, (uint32_t)c * 16u + 4u, 0));
+  v.z = __builtin_bit_cast(float, buf_load4(r, (uint32_t)c * 16u + 8u, 0));
+  v.w = __builtin_bit_cast(float, buf_load4(r, (uint32_t)c * 16u + 12u, 0));
   return v;
 }
 
@@ -146,8 +163,8 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi,
   lo = as_u32(l);
 }
 
-// hi/lo fp16 split of four activations written at column kl of rows 2r and
-// 2r+1 of the wave's slice; returns their exact fp32 sum (q4_1 block sums).
+// hi/lo split of four activations written at column kl of rows 2r and 2r+1
+// of the wave's slice; returns their fp32 sum (q4_1 block sums).
 __device__ __forceinline__ float stage4(_Float16* xs, int xstride, int r,
                                         int kl, float4 v) {
   uint2 hi, lo;
@@ -158,18 +175,27 @@ __device__ __forceinline__ float stage4(_Float16* xs, int xstride, int r,
   return (v.x + v.y) + (v.z + v.w);
 }
 
-template <int QT, int MR, int D>
+// Sum of 8 consecutive lanes' values (one 32-element block = 8 float4).
+__device__ __forceinline__ float block_sum8(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  return v;
+}
+
+template <int QT, int MR, int GW, bool RING>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int M = a.m;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int slice = wave;                       // K slice of this wave
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = K slice
   const int tile = blockIdx.x;
-  const int g0 = slice * a.gw;
-  const int g1 = min(a.g, g0 + a.gw);
-  const int ng = g1 - g0;
+  const int g0 = wave * a.gw;
+  const int ng = min(a.gw, a.g - g0);  // >= 1 (the planner guarantees it)
+  // groups processed: a whole number of ring passes (zero groups past ng)
+  const int nch = RING ? (ng + GW - 1) / GW : 1;
+  const int npad = nch * GW;
   const int n = lane & 15;   // W row within the tile (and MFMA A row)
   const int kq = lane >> 4;  // quarter of each block (and D row group)
 
@@ -178,57 +204,78 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   float* xsum = (float*)(wl + (size_t)2 * M * a.xstride * 2);
   float* part = (float*)(smem + (size_t)a.split * a.wave_lds);
 
-  // ---- activations of this wave's K range ---------------------------------
-  // M == 1 and a short range: loads are issued before the weight loads and
-  // held in registers, so converting them never waits on HBM.
-  const int c4 = ng * (kGroupK / 4);  // float4 per activation row of the slice
+  // ---- per-wave buffer ranges --------------------------------------------
+  const size_t unit0 = (size_t)tile * a.g + g0;
+  WaveRsrc rs;
+  rs.q = make_rsrc(a.qs + unit0 * unit_quant_bytes<QT>(),
+                   (uint32_t)ng * unit_quant_bytes<QT>());
+  rs.d = make_rsrc(a.d + unit0 * kUnitScaleBytes, (uint32_t)ng * kUnitScaleBytes);
+  rs.m = rs.d;
+  if (QT == MLQ_Q4_1)
+    rs.m = make_rsrc(a.mn + unit0 * kUnitScaleBytes, (uint32_t)ng * kUnitScaleBytes);
+  const uint32_t qoff = (uint32_t)lane * 16u;
+  const uint32_t soff = (uint32_t)n * 8u;
+
+  // ---- activations of the slice: loads first --------------------------------
+  // c4 float4 per staged activation row (npad groups); elements past the
+  // slice or past k read as zero.
   const int kbase = g0 * kGroupK;
+  const int c4 = npad * (kGroupK / 4);
+  const uint32_t xbytes = (uint32_t)min(ng * kGroupK, a.k - kbase) * 4u;
   const bool vec = (a.k & 3) == 0;
-  const bool x_in_regs = M == 1 && c4 <= kMaxXRegs * 64;
-  float4 xr[kMaxXRegs];
-  if (x_in_regs) {
+  // Register-held part: MR == 1 covers 4 float4 per lane (8 groups); MR > 1
+  // covers one float4 per lane of every row (2 groups). The rest, if any,
+  // is staged after the weight loads are issued.
+  constexpr int XR = MR == 1 ? kXRegs : kGemvMaxRows;
+  float4 xr[XR];
 #pragma unroll
-    for (int i = 0; i < kMaxXRegs; ++i) {
-      const int c = lane + 64 * i;
-      xr[i] = c < c4 ? load_x4(a.x, kbase + 4 * c, a.k, vec) : make_float4(0, 0, 0, 0);
+  for (int i = 0; i < XR; ++i) {
+    const int r = MR == 1 ? 0 : i;
+    const int c = MR == 1 ? lane + 64 * i : lane;
+    if (r < M && (MR > 1 || 64 * i < c4)) {  // wave-uniform
+      const rsrc_t rx = make_rsrc(a.x + (size_t)r * a.k + kbase, xbytes);
+      xr[i] = load_x4(rx, c < c4 ? c : 0x2000000, vec);
     }
   }
 
-  // ---- weight prologue: D groups in flight -------------------------------
-  const size_t unit0 = (size_t)tile * a.g + g0;
-  Slot<QT> ring[D];
+  // ---- weight loads: the first GW groups of the slice --------------------
+  // Issued group by group (not clustered by kind), so group 0 can start as
+  // soon as its own line and scales land.
+  Slot<QT> ring[GW];
 #pragma unroll
-  for (int s = 0; s < D; ++s) load_slot<QT>(a, ring[s], unit0 + min(s, ng - 1), lane);
+  for (int s = 0; s < GW; ++s) {
+    load_group<QT>(rs, ring[s], s, qoff, soff);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
-  // ---- stage hi/lo activations (+ q4_1 block sums: 8 float4 per block) ---
-  const int nblk_w = ng * kGroupBlocks;
-  if (x_in_regs) {
+  // ---- stage hi/lo activations (+ q4_1 block sums) -----------------------
+  const int nblk = npad * kGroupBlocks;
 #pragma unroll
-    for (int i = 0; i < kMaxXRegs; ++i) {
-      if (64 * i < c4) {  // wave-uniform
-        const int c = lane + 64 * i;
-        float sx = 0.0f;
-        if (c < c4) sx = stage4(xs, a.xstride, 0, 4 * c, xr[i]);
-        if (QT == MLQ_Q4_1) {
-          sx += __shfl_xor(sx, 1);
-          sx += __shfl_xor(sx, 2);
-          sx += __shfl_xor(sx, 4);
-          if (c < c4 && (c & 7) == 0) xsum[c >> 3] = sx;
-        }
+  for (int i = 0; i < XR; ++i) {
+    const int r = MR == 1 ? 0 : i;
+    const int c = MR == 1 ? lane + 64 * i : lane;
+    if (r < M && (MR > 1 || 64 * i < c4)) {  // wave-uniform
+      float sx = 0.0f;
+      if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, xr[i]);
+      if (QT == MLQ_Q4_1) {
+        sx = block_sum8(sx);
+        if (c < c4 && (c & 7) == 0) xsum[r * nblk + (c >> 3)] = sx;
       }
     }
-  } else {
+  }
+  // Slices longer than the register-held part (MR == 1: > 8 groups; MR > 1:
+  // > 2 groups): the remainder, after the weight loads are in flight.
+  const int c_done = MR == 1 ? 64 * XR : 64;
+  if (c4 > c_done) {
     for (int r = 0; r < M; ++r) {
-      const float* xrow = a.x + (size_t)r * a.k;
-      for (int c0 = 0; c0 < c4; c0 += 64) {
-        const int c = c0 + lane;
+      const rsrc_t rx = make_rsrc(a.x + (size_t)r * a.k + kbase, xbytes);
+      for (int cb = c_done; cb < c4; cb += 64) {
+        const int c = cb + lane;
         float sx = 0.0f;
-        if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, load_x4(xrow, kbase + 4 * c, a.k, vec));
+        if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, load_x4(rx, c, vec));
         if (QT == MLQ_Q4_1) {
-          sx += __shfl_xor(sx, 1);
-          sx += __shfl_xor(sx, 2);
-          sx += __shfl_xor(sx, 4);
-          if (c < c4 && (c & 7) == 0) xsum[r * nblk_w + (c >> 3)] = sx;
+          sx = block_sum8(sx);
+          if (c < c4 && (c & 7) == 0) xsum[r * nblk + (c >> 3)] = sx;
         }
       }
     }
@@ -244,54 +291,72 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const int r0 = 2 * kq, r1 = 2 * kq + 1;  // activation rows of this lane's D
   float acc0 = 0.0f, acc1 = 0.0f;
 
-  // One group: unpack the slot (B fragments, scales), optionally refill the
-  // slot's registers with group `refill` (its old contents are dead by then),
-  // then the four MFMAs and fp32 fixups.
-  auto group = [&](Slot<QT>& slot, int gl, bool do_refill, size_t refill) {
+  // Group j from `slot`: decode the B fragments, (ring) refill the slot with
+  // group j + GW, four MFMAs, then the fp32 fixups.
+  auto group = [&](Slot<QT>& slot, int j) {
     h8_t bfrag[kGroupBlocks];
-    float df[kGroupBlocks], mf[kGroupBlocks];
 #pragma unroll
-    for (int j = 0; j < kGroupBlocks; ++j) {
+    for (int b = 0; b < kGroupBlocks; ++b) {
       if (QT == MLQ_Q8_0) {
-        const uint4 q = (j < 2) ? slot.q : slot.q2;
-        bfrag[j] = decode8<QT>((j & 1) ? q.z : q.x, (j & 1) ? q.w : q.y);
+        const uint4 q = (b < 2) ? slot.q : slot.q2;
+        bfrag[b] = decode8<QT>((b & 1) ? q.z : q.x, (b & 1) ? q.w : q.y);
       } else {
-        const uint32_t w0 = j == 0 ? slot.q.x : j == 1 ? slot.q.y
-                          : j == 2 ? slot.q.z : slot.q.w;
-        bfrag[j] = decode8<QT>(w0, 0);
+        const uint32_t w0 = b == 0 ? slot.q.x : b == 1 ? slot.q.y
+                          : b == 2 ? slot.q.z : slot.q.w;
+        bfrag[b] = decode8<QT>(w0, 0);
       }
-      df[j] = scale_at(slot.d, j);
-      mf[j] = QT == MLQ_Q4_1 ? scale_at(slot.m, j) : 0.0f;
     }
-    if (do_refill) load_slot<QT>(a, slot, refill, lane);
+    const uint2 dd = slot.d;
+    const uint2 mm = slot.m;
+    if (RING) load_group<QT>(rs, slot, j + GW, qoff, soff);
+    const f4_t zero = {0.f, 0.f, 0.f, 0.f};
+    f4_t D[kGroupBlocks];
 #pragma unroll
-    for (int j = 0; j < kGroupBlocks; ++j) {
-      const uint4 av = *(const uint4*)(arow + gl * kGroupK + j * kQK);
-      const f4_t zero = {0.f, 0.f, 0.f, 0.f};
-      const f4_t dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          __builtin_bit_cast(h8_t, av), bfrag[j], zero, 0, 0, 0);
-      acc0 = fmaf(df[j], dd[0] + dd[1], acc0);
-      if (MR > 1) acc1 = fmaf(df[j], dd[2] + dd[3], acc1);
+    for (int b = 0; b < kGroupBlocks; ++b) {
+      const uint4 av = *(const uint4*)(arow + j * kGroupK + b * kQK);
+      D[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          __builtin_bit_cast(h8_t, av), bfrag[b], zero, 0, 0, 0);
+    }
+    float4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+    if (QT == MLQ_Q4_1) {
+      if (r0 < M) s0 = *(const float4*)(xsum + r0 * nblk + j * kGroupBlocks);
+      if (MR > 1 && r1 < M) s1 = *(const float4*)(xsum + r1 * nblk + j * kGroupBlocks);
+    }
+#pragma unroll
+    for (int b = 0; b < kGroupBlocks; ++b) {
+      const float df = (float)half_at(dd, b);
+      acc0 = fmaf(df, D[b][0] + D[b][1], acc0);
+      if (MR > 1) acc1 = fmaf(df, D[b][2] + D[b][3], acc1);
       if (QT == MLQ_Q4_1) {
-        const int b = gl * kGroupBlocks + j;
-        if (r0 < M) acc0 = fmaf(mf[j], xsum[r0 * ng * kGroupBlocks + b], acc0);
-        if (MR > 1 && r1 < M) acc1 = fmaf(mf[j], xsum[r1 * ng * kGroupBlocks + b], acc1);
+        const float mf = (float)half_at(mm, b);
+        const float e0 = b == 0 ? s0.x : b == 1 ? s0.y : b == 2 ? s0.z : s0.w;
+        acc0 = fmaf(mf, e0, acc0);
+        if (MR > 1) {
+          const float e1 = b == 0 ? s1.x : b == 1 ? s1.y : b == 2 ? s1.z : s1.w;
+          acc1 = fmaf(mf, e1, acc1);
+        }
       }
     }
   };
 
-  // Full chunks of D groups: every slot is consumed and refilled D groups
-  // ahead (refills past the range repeat the last group and are never used).
-  int gb = 0;
-  for (; gb + D <= ng; gb += D) {
+  // The scheduling barrier between groups keeps each group's LDS reads and
+  // temporaries local (hoisting them across groups costs registers, hence
+  // occupancy, for no gain: the weight lines are what the wave waits for).
+  if (RING) {
+    for (int jb = 0; jb < npad; jb += GW) {
 #pragma unroll
-    for (int s = 0; s < D; ++s)
-      group(ring[s], gb + s, true, unit0 + min(gb + s + D, ng - 1));
+      for (int s = 0; s < GW; ++s) {
+        group(ring[s], jb + s);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < GW; ++s) {
+      group(ring[s], s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
-  // Tail: the remaining groups are already in the ring; no more loads.
-#pragma unroll
-  for (int s = 0; s < D; ++s)
-    if (gb + s < ng) group(ring[s], gb + s, false, 0);
 
   // ---- output ------------------------------------------------------------
   if (a.split == 1) {
@@ -320,39 +385,53 @@ int env_int(const char* name, int fallback) {
   return v ? std::atoi(v) : fallback;
 }
 
-// Plan override: set through mlq_set_gemv_plan, initialised from the
-// MLQ_GEMV_SPLIT / MLQ_GEMV_DEPTH environment variables (0 = automatic).
+// Split override: set through mlq_set_gemv_split, initialised from the
+// MLQ_GEMV_SPLIT environment variable (0 = automatic).
 int g_split_override = -1;
-int g_depth_override = -1;
 
 int split_override() {
   if (g_split_override < 0) g_split_override = env_int("MLQ_GEMV_SPLIT", 0);
   return g_split_override;
 }
-int depth_override() {
-  if (g_depth_override < 0) g_depth_override = env_int("MLQ_GEMV_DEPTH", 0);
-  return g_depth_override;
-}
 
 struct Plan {
-  int split, gw, depth;
+  int split, gw;
+  int depth;  // GW: groups in flight per wave (1..8)
+  bool ring;  // slices longer than 8 groups: ring of 8 slots
+  int padded; // groups staged per wave (gw, or whole ring passes)
   size_t wave_lds, lds;
 };
 
+// Groups in flight per wave without spilling (VGPR budget of a 1024-thread
+// workgroup): every group of the slice when gw <= max_depth, else a ring of
+// ring_depth slots. q4_1 carries mins and block sums per group.
+constexpr int kMaxDepth = 8;
+int max_depth(int type, int m) {
+  if (type == MLQ_Q4_1) return m == 1 ? 6 : 3;
+  return kMaxDepth;
+}
+constexpr int ring_depth(int type, int mr) {
+  return type == MLQ_Q4_1 ? (mr == 1 ? 4 : 2) : 8;
+}
+
+// Groups a wave of `gw` processes (and stages activations for).
+int padded_groups(int type, int m, int gw) {
+  if (gw <= max_depth(type, m)) return gw;
+  const int rd = ring_depth(type, m == 1 ? 1 : kGemvMaxRows);
+  return (gw + rd - 1) / rd * rd;
+}
+
 size_t wave_lds_bytes(int type, int m, int gw) {
-  const size_t xstride = (size_t)gw * kGroupK + kRowPadHalves;
+  const int pg = padded_groups(type, m, gw);
+  const size_t xstride = (size_t)pg * kGroupK + kRowPadHalves;
   size_t b = (size_t)2 * m * xstride * 2;
-  if (type == MLQ_Q4_1) b += (size_t)m * gw * kGroupBlocks * 4;
+  if (type == MLQ_Q4_1) b += (size_t)m * pg * kGroupBlocks * 4;
   return (b + 15) / 16 * 16;
 }
 
 Plan make_plan(int type, int m, const Geometry& geo) {
   Plan p;
   const int env_split = split_override();
-  const int env_depth = depth_override();
-  int depth = env_depth;
-  if (depth != 2 && depth != 4 && depth != 8) depth = 8;
-  p.depth = depth;
   // Default split: enough waves for the whole grid to be resident at about
   // 16 waves per CU, but at least two groups per wave.
   int split = 1;
@@ -378,47 +457,54 @@ Plan make_plan(int type, int m, const Geometry& geo) {
   p.split = (geo.g + p.gw - 1) / p.gw;
   p.lds = p.wave_lds * p.split +
           (p.split > 1 ? (size_t)p.split * m * kTileRows * 4 : 0);
+  // Every group of the slice in flight at once (depth = gw) when it fits,
+  // otherwise the ring.
+  p.ring = p.gw > max_depth(type, m);
+  p.depth = p.ring ? ring_depth(type, m == 1 ? 1 : kGemvMaxRows) : p.gw;
+  p.padded = padded_groups(type, m, p.gw);
   return p;
 }
 
-template <int QT, int MR, int D>
+template <int QT, int MR, int GW, bool RING>
 hipError_t launch_typed(const GemvArgs& a, size_t lds, hipStream_t stream) {
   // Opt in to more than the default 64 KiB of dynamic LDS when needed.
   static size_t configured = 64 * 1024;
   if (lds > configured) {
-    hipError_t e = hipFuncSetAttribute((const void*)gemv_kernel<QT, MR, D>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
+    hipError_t e = hipFuncSetAttribute(
+        (const void*)gemv_kernel<QT, MR, GW, RING>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     configured = lds;
   }
-  gemv_kernel<QT, MR, D><<<a.nt, 64 * a.split, lds, stream>>>(a);
+  gemv_kernel<QT, MR, GW, RING><<<a.nt, 64 * a.split, lds, stream>>>(a);
   return hipGetLastError();
 }
 
 template <int QT, int MR>
-hipError_t launch_depth(const GemvArgs& a, int depth, size_t lds,
-                        hipStream_t stream) {
-  switch (depth) {
-    case 2: return launch_typed<QT, MR, 2>(a, lds, stream);
-    case 4: return launch_typed<QT, MR, 4>(a, lds, stream);
-    default: return launch_typed<QT, MR, 8>(a, lds, stream);
+hipError_t launch_depth(const GemvArgs& a, const Plan& p, hipStream_t stream) {
+  if (p.ring) return launch_typed<QT, MR, ring_depth(QT, MR), true>(a, p.lds, stream);
+  // (depths above max_depth(QT, m) are never planned)
+  switch (p.depth) {
+    case 1: return launch_typed<QT, MR, 1, false>(a, p.lds, stream);
+    case 2: return launch_typed<QT, MR, 2, false>(a, p.lds, stream);
+    case 3: return launch_typed<QT, MR, 3, false>(a, p.lds, stream);
+    case 4: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 4, false>(a, p.lds, stream);
+    case 5: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 5, false>(a, p.lds, stream);
+    case 6: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 6, false>(a, p.lds, stream);
+    case 7: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 7, false>(a, p.lds, stream);
+    default: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 8, false>(a, p.lds, stream);
   }
 }
 
 template <int QT>
-hipError_t launch_rows(const GemvArgs& a, int depth, size_t lds,
-                       hipStream_t stream) {
-  if (a.m == 1) return launch_depth<QT, 1>(a, depth, lds, stream);
-  return launch_depth<QT, kGemvMaxRows>(a, depth, lds, stream);
+hipError_t launch_rows(const GemvArgs& a, const Plan& p, hipStream_t stream) {
+  if (a.m == 1) return launch_depth<QT, 1>(a, p, stream);
+  return launch_depth<QT, kGemvMaxRows>(a, p, stream);
 }
 
 }  // namespace
 
-void set_gemv_plan(int split, int depth) {
-  g_split_override = split;
-  g_depth_override = depth;
-}
+void set_gemv_split(int split) { g_split_override = split; }
 
 int gemv_max_k(int type, int m) {
   if (m < 1 || m > kGemvMaxRows) return 0;
@@ -440,10 +526,8 @@ hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
   if (p.lds > lds_limit()) return hipErrorInvalidValue;
   GemvArgs a;
   a.qs = (const uint8_t*)w.base + w.qs_off;
-  a.d = (const uint16_t*)((const uint8_t*)w.base + w.d_off);
-  a.mn = w.type == MLQ_Q4_1
-             ? (const uint16_t*)((const uint8_t*)w.base + w.m_off)
-             : nullptr;
+  a.d = (const uint8_t*)w.base + w.d_off;
+  a.mn = w.type == MLQ_Q4_1 ? (const uint8_t*)w.base + w.m_off : nullptr;
   a.x = x;
   a.y = y;
   a.m = m;
@@ -453,12 +537,12 @@ hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
   a.nt = geo.nt;
   a.split = p.split;
   a.gw = p.gw;
-  a.xstride = p.gw * kGroupK + kRowPadHalves;
+  a.xstride = p.padded * kGroupK + kRowPadHalves;
   a.wave_lds = (int)p.wave_lds;
   switch (w.type) {
-    case MLQ_Q8_0: return launch_rows<MLQ_Q8_0>(a, p.depth, p.lds, stream);
-    case MLQ_Q4_0: return launch_rows<MLQ_Q4_0>(a, p.depth, p.lds, stream);
-    default: return launch_rows<MLQ_Q4_1>(a, p.depth, p.lds, stream);
+    case MLQ_Q8_0: return launch_rows<MLQ_Q8_0>(a, p, stream);
+    case MLQ_Q4_0: return launch_rows<MLQ_Q4_0>(a, p, stream);
+    default: return launch_rows<MLQ_Q4_1>(a, p, stream);
   }
 }
 

@@ -23,8 +23,8 @@ hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream);
 // Largest k the GEMV accepts for m rows (LDS-bound).
 int gemv_max_k(int type, int m);
-// Plan override (0 = automatic); validated by the caller.
-void set_gemv_plan(int split, int depth);
+// Split override (0 = automatic); validated by the caller.
+void set_gemv_split(int split);
 
 // gemm_mfma.hip: any m >= 1.
 hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,

@@ -175,14 +175,16 @@ def test_linear_matches_oracle(pkg, oracle, cuda, qtype, m, n, k):
 
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("split", [0, 1, 2, 4, 8, 16])
-@pytest.mark.parametrize("depth", [2, 4, 8])
-def test_gemv_every_plan(pkg, oracle, cuda, qtype, split, depth):
-    """Every GEMV decomposition (K split x load depth) on shapes whose runs
-    exceed the depth (exercising the refill ring) and have ragged tails."""
-    _print_case(test="gemv_plan", qtype=qtype, split=split, depth=depth)
-    pkg.set_gemv_plan(split, depth)
+def test_gemv_every_split(pkg, oracle, cuda, qtype, split):
+    """Every GEMV K split on shapes that take each code path: slices of
+    1..8 groups all in flight, slices longer than the in-flight budget (the
+    refill ring), a shorter last slice (groups % split != 0), k % 4 != 0
+    (element-wise activation loads) and 1, 2, 3 and 8 activation rows."""
+    _print_case(test="gemv_split", qtype=qtype, split=split)
+    pkg.set_gemv_split(split)
     try:
-        for m, n, k in [(1, 48, 4000), (3, 40, 2100), (8, 17, 1500)]:
+        for m, n, k in [(1, 48, 4000), (3, 40, 2100), (8, 17, 1500),
+                        (2, 20, 1001), (1, 33, 9000)]:
             blocks = make_blocks(qtype, n, k, seed=n + k + m)
             x = make_x(m, k, seed=k + 3)
             tw = pkg.upload(qtype, blocks, n, k, device=cuda)
@@ -191,7 +193,7 @@ def test_gemv_every_plan(pkg, oracle, cuda, qtype, split, depth):
             rep = error_report(got, ref, x, k)
             assert np.isfinite(got).all() and rep["max_abs_over_atol"] < 0.05, (m, n, k, rep)
     finally:
-        pkg.set_gemv_plan(0, 0)
+        pkg.set_gemv_split(0)
 
 
 @pytest.mark.parametrize("qtype", TYPES)
