@@ -13,6 +13,13 @@ Also reported in the same line: the q8_0 prefill GEMM (configs[4], M=512,
 W [11008, 4096]) in TFLOP/s against the dense fp16 MFMA peak, and the
 reference CPU path (the oracle restatement) timed on the host cores.
 `--all` adds every BASELINE configuration and the 196-GEMV decode sweep.
+
+Profiling modes (one kernel family per run, for rocprofv3 counter passes):
+`--mode headline` launches only the headline GEMV (eagerly with `--eager`),
+`--mode copy` runs a plain device-to-device copy of 256 MiB, the known-size
+reference that scales the FETCH_SIZE / WRITE_SIZE counters to bytes.
+`roofline.traffic` is read from profiles/hbm_traffic_gemv_q4_0_c1.md (the
+summary of those counter runs) when it is present, else null.
 """
 from __future__ import annotations
 
@@ -31,6 +38,8 @@ import __graft_entry__ as graft  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 512 << 20
+COPY_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_gemv_q4_0_c1.md")
 
 GGUF_BLOCK = {"q8_0": 34, "q4_0": 18, "q4_1": 20}
 
@@ -92,14 +101,44 @@ def time_graph(torch, launch, steps, warmup):
     return start.elapsed_time(end) / 1e3
 
 
+def time_eager(torch, launch, steps, warmup):
+    """Plain back-to-back launches on one stream (what counter passes see)."""
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(max(warmup, 1)):
+            launch(i)
+        stream.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(steps):
+            launch(i)
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3
+
+
+def read_traffic():
+    """HBM bytes per launch of the headline kernel, from the committed
+    counter summary (a line `traffic_bytes_per_launch: N`), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1].strip()))
+    except OSError:
+        return None
+    return None
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed):
+def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed, eager=False):
     log(f"{qtype} m={m} n={n} k={k}: setup")
     c = Case(pkg, torch, qtype, m, n, k, seed)
-    sec = time_graph(torch, c.launch, steps, warmup)
+    sec = (time_eager if eager else time_graph)(torch, c.launch, steps, warmup)
     per = sec / steps
     out = {"qtype": qtype, "m": m, "n": n, "k": k, "copies": len(c.weights),
            "us_per_call": per * 1e6,
@@ -181,6 +220,10 @@ def main():
                     help="also run every BASELINE config and the decode sweep")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--mode", choices=["full", "headline", "copy"],
+                    default="full", help="headline/copy: profiling runs")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch eagerly instead of replaying a HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (no multi-GPU path); "
@@ -192,8 +235,21 @@ def main():
     pkg.lib()
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
 
+    if args.mode == "copy":
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        sec = time_eager(torch, lambda i: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"mode": "copy", "bytes_read": COPY_BYTES,
+                          "bytes_written": COPY_BYTES,
+                          "us_per_copy": sec / args.steps * 1e6}), flush=True)
+        return
     head = bench_case(pkg, torch, "q4_0", 1, 18944, 3584, args.steps,
-                      args.warmup, seed=1000)
+                      args.warmup, seed=1000, eager=args.eager)
+    if args.mode == "headline":
+        print(json.dumps({"mode": "headline", **head}), flush=True)
+        return
     pre_steps = max(10, min(200, args.steps // 5))
     prefill = bench_case(pkg, torch, "q8_0", 512, 11008, 4096, pre_steps,
                          min(args.warmup, 5), seed=4000)
@@ -218,7 +274,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": read_traffic()},
         "prefill": {"workload": "configs[4]: q8_0 GEMM W[11008,4096] x "
                                 "X[512,4096] fp32",
                     "us_per_call": round(prefill["us_per_call"], 2),
