@@ -133,6 +133,22 @@ int mlq_dequantize(const mlq_weight* w, int row0, int rows, float* out,
 int mlq_linear(const mlq_weight* w, const float* x, float* y, int m,
                mlq_stream_t stream);
 
+/* Device workspace bytes mlq_linear_ws needs for m activation rows with
+ * weight w (*bytes = 0 when the kernels for that shape need none: the decode
+ * GEMV). The prefill GEMM uses it for a one-pass fp16 copy of x, which
+ * halves the activation bytes its stages move. */
+int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes);
+
+/* mlq_linear with a caller workspace of at least mlq_linear_workspace(w, m)
+ * bytes (device memory, 256-byte aligned; contents need no initialisation
+ * and are scratch for the duration of the call). MLQ_ERR_BUFFER_TOO_SMALL
+ * when it is smaller. Calls that share one workspace must be ordered (same
+ * stream), like any other buffer. Same result contract as mlq_linear (fp16
+ * rounding of x happens in both prefill variants). No counterpart in the
+ * reference (its kernels take fp32 x directly, src/cuda_quant.cu:78-182). */
+int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
+                  void* workspace, size_t workspace_bytes, mlq_stream_t stream);
+
 /* Raw GGUF AoS blocks in device memory: the meaning of the `const void*`
  * weight of cudaQ*LinearDeviceWeight / cudaQ*LinearDeviceInput
  * (src/cuda_quant.cu:300-361). The blocks are repacked into `workspace`

@@ -76,6 +76,8 @@ SIGNATURES = {
     "mlq_linear": ([_WP, _P, _P, _I, _P], _I),
     "mlq_linear_aos": ([_I, _P, _Z, _I, _I, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_linear_path": ([_WP, _P, _P, _I, _I, _P], _I),
+    "mlq_linear_workspace": ([_WP, _I, ctypes.POINTER(_Z)], _I),
+    "mlq_linear_ws": ([_WP, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
     "mlq_set_gemv_split": ([_I], _I),
 }
@@ -209,8 +211,37 @@ def dequantize(w: TiledWeight, row0: int = 0, rows: int | None = None,
     return out
 
 
-def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None):
-    """y[m, n] = x[m, k] @ W^T on the device (x fp32 contiguous, 1-D or 2-D)."""
+def workspace_bytes(w: TiledWeight, m: int) -> int:
+    """Device workspace mlq_linear_ws needs for m activation rows."""
+    nbytes = ctypes.c_size_t(0)
+    _check(lib().mlq_linear_workspace(ctypes.byref(w.layout), m,
+                                      ctypes.byref(nbytes)),
+           "mlq_linear_workspace")
+    return nbytes.value
+
+
+_WORKSPACES: dict = {}
+
+
+def _workspace(device, nbytes: int):
+    """Grow-only per-device workspace for `linear` (calls on one device share
+    it, so they must be ordered on one stream; pass `workspace=` otherwise)."""
+    import torch
+    key = torch.device(device).index or 0
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = buf
+    return buf
+
+
+def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None,
+           workspace="auto"):
+    """y[m, n] = x[m, k] @ W^T on the device (x fp32 contiguous, 1-D or 2-D).
+
+    path AUTO with a workspace (the default "auto" takes the per-device one)
+    runs mlq_linear_ws; workspace=None, or a forced path, runs
+    mlq_linear_path (the prefill GEMM then reads fp32 x directly)."""
     import torch
     if x.dtype != torch.float32 or not x.is_contiguous():
         raise ValueError("x must be a contiguous float32 device tensor")
@@ -221,6 +252,17 @@ def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None):
     if y is None:
         shape = (w.n,) if x.dim() == 1 else (m, w.n)
         y = torch.empty(shape, dtype=torch.float32, device=x.device)
+    if path == PATH_AUTO and workspace is not None:
+        need = workspace_bytes(w, m)
+        ws = workspace
+        if isinstance(workspace, str):
+            ws = _workspace(x.device, need) if need else None
+        ws_ptr = ws.data_ptr() if ws is not None else None
+        ws_len = ws.numel() * ws.element_size() if ws is not None else 0
+        _check(lib().mlq_linear_ws(ctypes.byref(w.layout), x.data_ptr(),
+                                   y.data_ptr(), m, ws_ptr, ws_len,
+                                   _stream(stream)), "mlq_linear_ws")
+        return y
     _check(lib().mlq_linear_path(ctypes.byref(w.layout), x.data_ptr(),
                                  y.data_ptr(), m, path, _stream(stream)),
            "mlq_linear")

@@ -4,6 +4,7 @@
 // synchronize.
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstring>
 
 #include "kernels/launch.h"
@@ -47,6 +48,12 @@ int check_tiled(const mlq_weight* w) {
       w->bytes < expect.bytes)
     return MLQ_ERR_INVALID_ARG;
   return MLQ_OK;
+}
+
+// The automatic kernel choice: the decode GEMV for up to kGemvMaxRows rows
+// when its activation staging fits LDS, the MFMA GEMM otherwise.
+bool uses_gemv(const mlq_weight* w, int m) {
+  return m <= kGemvMaxRows && w->k <= gemv_max_k(w->type, m);
 }
 
 }  // namespace
@@ -173,7 +180,7 @@ int mlq_linear_path(const mlq_weight* w, const float* x, float* y, int m,
   if (rc != MLQ_OK) return rc;
   if (x == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
-  const bool gemv_fits = m <= kGemvMaxRows && w->k <= gemv_max_k(w->type, m);
+  const bool gemv_fits = uses_gemv(w, m);
   bool use_gemv;
   switch (path) {
     case MLQ_PATH_AUTO: use_gemv = gemv_fits; break;
@@ -192,6 +199,31 @@ int mlq_linear_path(const mlq_weight* w, const float* x, float* y, int m,
 int mlq_linear(const mlq_weight* w, const float* x, float* y, int m,
                mlq_stream_t stream) {
   return mlq_linear_path(w, x, y, m, MLQ_PATH_AUTO, stream);
+}
+
+int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes) {
+  int rc = check_tiled(w);
+  if (rc != MLQ_OK) return rc;
+  if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (m <= 0) return MLQ_ERR_SHAPE;
+  *bytes = uses_gemv(w, m) ? 0 : gemm_workspace_bytes(m, w->k);
+  return MLQ_OK;
+}
+
+int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
+                  void* workspace, size_t workspace_bytes,
+                  mlq_stream_t stream) {
+  int rc = check_tiled(w);
+  if (rc != MLQ_OK) return rc;
+  if (x == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (m <= 0) return MLQ_ERR_SHAPE;
+  const hipStream_t s = (hipStream_t)stream;
+  if (uses_gemv(w, m)) return hip_status(launch_gemv(*w, x, y, m, s));
+  const size_t need = gemm_workspace_bytes(m, w->k);
+  if (workspace == nullptr || workspace_bytes < need)
+    return MLQ_ERR_BUFFER_TOO_SMALL;
+  if (((uintptr_t)workspace & 255u) != 0) return MLQ_ERR_INVALID_ARG;
+  return hip_status(launch_gemm_ws(*w, x, y, m, workspace, workspace_bytes, s));
 }
 
 int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,

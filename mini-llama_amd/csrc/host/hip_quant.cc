@@ -115,6 +115,17 @@ void* aosWorkspace(int device_id, size_t bytes) {
   return buf.data();
 }
 
+// Grow-only per-device workspace for the prefill GEMM's fp16 copy of x
+// (mlq_linear_ws). Null-stream ordering makes reuse across calls safe.
+void* activationWorkspace(int device_id, size_t bytes) {
+  static std::mutex mu;
+  static std::map<int, HipDeviceBuffer> buffers;
+  std::lock_guard<std::mutex> lock(mu);
+  HipDeviceBuffer& buf = buffers[device_id];
+  if (buf.bytes() < bytes) buf.reset(bytes, device_id);
+  return buf.data();
+}
+
 // Runs y = x W^T for a device weight pointer: a registered tiled buffer goes
 // straight to the kernels, anything else is taken as GGUF AoS blocks.
 void runLinear(int type, const void* w_dev, size_t block_count,
@@ -128,7 +139,11 @@ void runLinear(int type, const void* w_dev, size_t block_count,
       throw std::runtime_error(std::string(caller) +
                                ": uploaded weight has a different type or shape");
     }
-    rc = mlq_linear(&layout, x, y, p.rows, nullptr);
+    size_t ws_bytes = 0;
+    rc = mlq_linear_workspace(&layout, p.rows, &ws_bytes);
+    checkStatus(rc, caller);
+    void* ws = ws_bytes ? activationWorkspace(device_id, ws_bytes) : nullptr;
+    rc = mlq_linear_ws(&layout, x, y, p.rows, ws, ws_bytes, nullptr);
   } else {
     mlq_weight need;
     rc = mlq_weight_layout(type, p.out_features, p.in_features, &need);
@@ -291,9 +306,13 @@ HipTensor hipLinearUploaded(const HipTensor& x, const HipUploadedWeight& weight,
   hipSetDeviceId(device_id);
   const LinearParams p = computeLinearParams(x.shape(), weight.shape);
   HipTensor y(outputShape(p), device_id);
-  checkStatus(mlq_linear(&weight.layout, static_cast<const float*>(x.data()),
-                         static_cast<float*>(y.data()), p.rows, nullptr),
-              "mlq_linear");
+  size_t ws_bytes = 0;
+  checkStatus(mlq_linear_workspace(&weight.layout, p.rows, &ws_bytes), kCaller);
+  void* ws = ws_bytes ? activationWorkspace(device_id, ws_bytes) : nullptr;
+  checkStatus(mlq_linear_ws(&weight.layout, static_cast<const float*>(x.data()),
+                            static_cast<float*>(y.data()), p.rows, ws, ws_bytes,
+                            nullptr),
+              "mlq_linear_ws");
   return y;
 }
 

@@ -7,19 +7,23 @@
 //    64 x 64 = 2 x 2 v_mfma_f32_32x32x16_f16 (fp32 accumulate). The 32x32
 //    shape does twice the work per operand register of 16x16x32, which
 //    halves the LDS read traffic per flop.
-//  - K advances in stages of 64 (half of a 128-k group). Each stage's
-//    activations (fp32 -> fp16) and weights (codes decoded exactly, then
-//    scaled by d in fp16: one rounding, like d*q rounded to fp16) are
-//    written to LDS in row-major [row][k] slabs with a 16-byte row pad, so
-//    every MFMA operand is one conflict-free ds_read_b128.
-//  - Two LDS buffers and two register stages: while the waves run stage s
-//    from one LDS buffer, stage s+1 (requested a stage earlier) is converted
-//    from registers into the other, and stage s+2 is being fetched; one
-//    barrier per stage.
-//  - 72 KiB of LDS and <= 256 VGPRs per lane, so two workgroups share a CU and one's
-//    decode work overlaps the other's MFMAs.
+//  - K advances in stages of 64 (half of a 128-k group). Activations are
+//    converted fp32 -> fp16 into an LDS slab [row][k] with a 16-byte row pad
+//    (every A fragment is one conflict-free ds_read_b128).
+//  - Weights never touch LDS: with 64 x 64 wave tiles, LDS fragment reads
+//    cost as much as the MFMAs themselves on this part (~128 B/clk per CU),
+//    so each wave loads its own B fragments straight from the tiled layout
+//    (two 16-byte chunks per lane cover a stage's four k steps) and decodes
+//    them in registers (codes exact, then scaled by d in fp16: one
+//    rounding, like d*q rounded to fp16). Halves LDS traffic per flop.
+//  - A register ring of two stages: stage s+2 is requested while stage s
+//    runs on the MFMAs and stage s+1's activations go into the other LDS
+//    buffer; one barrier per stage.
 //  - Workgroups are numbered XCD-major: the four m-tiles of one weight
 //    column block run on the same XCD and share its L2.
+//  - With a workspace, x is first converted once to an fp16 copy
+//    (x_to_f16_kernel): the GEMM then moves half the activation bytes per
+//    stage and does no conversion work. Without one it reads fp32 x.
 // The scale is applied before the MFMA (per weight), so no per-block fixup
 // of the accumulators is needed; that is what keeps VALU work independent of
 // m (an int8 MFMA variant would need a per-(m, n, block) fp32 fixup).
@@ -35,7 +39,7 @@ namespace {
 constexpr int kBM = 128;           // x rows per workgroup
 constexpr int kBN = 128;           // W rows per workgroup (8 row tiles)
 constexpr int kBK = 64;            // k per stage
-constexpr int kTiles = kBN / kTileRows;
+constexpr int kTiles = kBN / kTileRows;  // 8: wave column block j covers tiles 4wn+2j, +1
 constexpr int kThreads = 256;
 constexpr int kStride = kBK + 8;   // halves per LDS row (144 B)
 constexpr int kXcds = 8;
@@ -46,19 +50,34 @@ struct GemmArgs {
   const uint8_t* qs;
   const uint8_t* d;
   const uint8_t* mn;
-  const float* x;
+  const float* x;      // fp32 activations [m][k] (XF32 modes)
+  const _Float16* xh;  // fp16 activations [m][kp] (XF16 mode, workspace)
   float* y;
   int m, n, k, g, nt;
+  int kp;              // row stride of xh: k rounded up to whole stages
   int mtiles, ntiles;  // workgroup grid
 };
 
-// Registers holding one stage of global data for this thread.
+// Activation source: fp32 rows loaded as float4 (k % 4 == 0), fp32 loaded
+// element by element, or the fp16 copy made by x_to_f16 in a workspace.
+enum XMode { kXF32Vec = 0, kXF32Scalar = 1, kXF16 = 2 };
+
+// Activations of one stage held in registers by one thread: rows t/16 + 16j,
+// k 4*(t%16) .. +3 of the stage.
+struct XStage {
+  float4 xa[8];  // fp32 modes
+  uint4 xh[4];   // fp16 mode: rows t/8 + 32j, k 8*(t%8) .. +7
+};
+
+// Weight fragments of one stage held in registers by one lane of one wave:
+// for each of the wave's two 32-column blocks j, two 16-byte (q8) or 8-byte
+// (q4) chunks of the tiled layout (quarters kq = o and 2 + o, o = lane/32)
+// and the fp16 scales (and mins) of the stage's two blocks.
 template <int QT>
-struct Stage {
-  float4 xa[8];   // activations: rows t/16 + 16j, k 4*(t%16) .. +3
-  uint4 q[2];     // weight chunks (q8: 16 B; q4: 8 B in .x/.y)
-  uint32_t dd[2]; // two fp16 scales (blocks 2h, 2h+1) per chunk
-  uint32_t mm[2]; // two fp16 mins (q4_1)
+struct WStage {
+  uint4 c[2][2];
+  uint32_t dd[2];
+  uint32_t mm[2];
 };
 
 __device__ __forceinline__ h2_t h2_splat(uint32_t bits16) {
@@ -70,18 +89,25 @@ __device__ __forceinline__ h2_t h2_splat(uint32_t bits16) {
 // either wholly inside the range or wholly past it. Otherwise each element
 // is loaded (and range-checked) on its own. A compile-time choice: a runtime
 // branch around the loads makes the compiler wait for each load in turn.
-template <int QT, bool VEC>
-__device__ __forceinline__ void load_stage(const GemmArgs& a, Stage<QT>& st,
-                                           rsrc_t rx, rsrc_t rq, rsrc_t rd,
-                                           rsrc_t rm, int s, int tid) {
+template <int XM>
+__device__ __forceinline__ void load_x(const GemmArgs& a, XStage& st, rsrc_t rx,
+                                       int s, int tid) {
   const int k0 = s * kBK;
-  // activations: 8 float4 per thread (zeros past the last row via the range)
+  if (XM == kXF16) {
+    const int c = tid & 7;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = (tid >> 3) + 32 * j;
+      st.xh[j] = buf_load16(rx, (uint32_t)((r * a.kp + k0 + 8 * c) * 2), 0);
+    }
+    return;
+  }
   const int c = tid & 15;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int r = (tid >> 4) + 16 * j;
     const uint32_t off = (uint32_t)((r * a.k + k0 + 4 * c) * 4);
-    if (VEC) {
+    if (XM == kXF32Vec) {
       st.xa[j] = __builtin_bit_cast(float4, buf_load16(rx, off, 0));
     } else {
       st.xa[j].x = __builtin_bit_cast(float, buf_load4(rx, off, 0));
@@ -90,31 +116,22 @@ __device__ __forceinline__ void load_stage(const GemmArgs& a, Stage<QT>& st,
       st.xa[j].w = __builtin_bit_cast(float, buf_load4(rx, off + 12, 0));
     }
   }
-  // weights: half-group h of group gi for 8 row tiles, two chunks per thread
-  const int gi = s >> 1, h = s & 1;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int wt = (tid >> 6) + 4 * j;  // row tile within the workgroup
-    const int lane = tid & 63;
-    const uint32_t unit = (uint32_t)(wt * a.g + gi);
-    if (QT == MLQ_Q8_0) {
-      st.q[j] = buf_load16(rq, ((unit * 2 + h) * 64 + lane) * 16, 0);
-    } else {
-      const uint2 v = buf_load8(rq, (unit * 64 + lane) * 16 + 8 * h, 0);
-      st.q[j] = make_uint4(v.x, v.y, 0, 0);
-    }
-    const uint32_t soff = ((unit * kTileRows + (lane & 15)) * 4 + 2 * h) * 2;
-    st.dd[j] = buf_load4(rd, soff, 0);
-    if (QT == MLQ_Q4_1) st.mm[j] = buf_load4(rm, soff, 0);
-  }
 }
 
-// Converts a stage held in registers into LDS (fp16 activations, fp16
-// pre-scaled weights).
-template <int QT>
-__device__ __forceinline__ void store_stage(const GemmArgs& a, Stage<QT>& st,
-                                            _Float16* as, _Float16* bs, int s,
-                                            int tid) {
+// Activations of a stage into the LDS slab [row][k] (fp32 modes convert;
+// the fp16 copy is already zero past k).
+template <int XM>
+__device__ __forceinline__ void store_x(const GemmArgs& a, XStage& st,
+                                        _Float16* as, int s, int tid) {
+  if (XM == kXF16) {
+    const int c = tid & 7;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = (tid >> 3) + 32 * j;
+      *(uint4*)(as + r * kStride + 8 * c) = st.xh[j];
+    }
+    return;
+  }
   const int k0 = s * kBK;
   const int c = tid & 15;
   // k tail: elements at or past k are zero (the row's next elements belong
@@ -137,65 +154,86 @@ __device__ __forceinline__ void store_stage(const GemmArgs& a, Stage<QT>& st,
     hv.y = pack_h2(st.xa[j].z, st.xa[j].w);
     *(uint2*)(as + r * kStride + 4 * c) = hv;
   }
+}
+
+// The MFMA B operand of v_mfma_f32_32x32x16_f16 for lane L is column L%32
+// (W row 16t + n of this wave's block j: t = 4wn + 2j + (L%32)/16,
+// n = L%16) at k octet o = L/32 of the 16-k step. In the tiled layout that
+// octet is quarter kq = 2*(ks%2) + o of block 2h + ks/2 (stage = half h of
+// group gi): the lane's chunks at lane n + 16*o and n + 16*(2+o) of the
+// tile's line hold all four k steps of the stage.
+template <int QT>
+__device__ __forceinline__ void load_w(const GemmArgs& a, WStage<QT>& st,
+                                       rsrc_t rq, rsrc_t rd, rsrc_t rm, int s,
+                                       int lane, int wn) {
+  const int gi = s >> 1, h = s & 1;
+  const int n = lane & 15, o = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int wt = (tid >> 6) + 4 * j;
-    const int lane = tid & 63;
-    const int n = wt * kTileRows + (lane & 15), kq = lane >> 4;
-    const h2_t d0 = h2_splat(st.dd[j] & 0xffffu), d1 = h2_splat(st.dd[j] >> 16);
-    uint4 o0, o1;  // block 2h (k 8kq..), block 2h+1 (k 32+8kq..)
-    if (QT == MLQ_Q8_0) {
-      const h2_t b = {(_Float16)1152.0f, (_Float16)1152.0f};
-      uint32_t p[8];
-      q8_pairs(st.q[j].x, p[0], p[1]);
-      q8_pairs(st.q[j].y, p[2], p[3]);
-      q8_pairs(st.q[j].z, p[4], p[5]);
-      q8_pairs(st.q[j].w, p[6], p[7]);
-      o0.x = as_u32((as_h2(p[0]) - b) * d0);
-      o0.y = as_u32((as_h2(p[1]) - b) * d0);
-      o0.z = as_u32((as_h2(p[2]) - b) * d0);
-      o0.w = as_u32((as_h2(p[3]) - b) * d0);
-      o1.x = as_u32((as_h2(p[4]) - b) * d1);
-      o1.y = as_u32((as_h2(p[5]) - b) * d1);
-      o1.z = as_u32((as_h2(p[6]) - b) * d1);
-      o1.w = as_u32((as_h2(p[7]) - b) * d1);
-    } else {
-      const float lo = QT == MLQ_Q4_0 ? 1032.0f : 1024.0f;
-      const float hi = QT == MLQ_Q4_0 ? 72.0f : 64.0f;
-      const h2_t blo = {(_Float16)lo, (_Float16)lo};
-      const h2_t bhi = {(_Float16)hi, (_Float16)hi};
-      const Q4Pairs p = q4_pairs(st.q[j].x);
-      const Q4Pairs r = q4_pairs(st.q[j].y);
-      if (QT == MLQ_Q4_0) {
-        o0.x = as_u32((as_h2(p.p0) - blo) * d0);
-        o0.y = as_u32((as_h2(p.p1) - bhi) * d0);
-        o0.z = as_u32((as_h2(p.p2) - blo) * d0);
-        o0.w = as_u32((as_h2(p.p3) - bhi) * d0);
-        o1.x = as_u32((as_h2(r.p0) - blo) * d1);
-        o1.y = as_u32((as_h2(r.p1) - bhi) * d1);
-        o1.z = as_u32((as_h2(r.p2) - blo) * d1);
-        o1.w = as_u32((as_h2(r.p3) - bhi) * d1);
+    const int t = 4 * wn + 2 * j + ((lane >> 4) & 1);
+    const uint32_t unit = (uint32_t)(t * a.g + gi);
+#pragma unroll
+    for (int ci = 0; ci < 2; ++ci) {
+      const int lq = n + 16 * (2 * ci + o);  // lane of the line holding kq
+      if (QT == MLQ_Q8_0) {
+        st.c[j][ci] = buf_load16(rq, ((unit * 2 + h) * 64 + lq) * 16, 0);
       } else {
-        const h2_t m0 = h2_splat(st.mm[j] & 0xffffu), m1 = h2_splat(st.mm[j] >> 16);
-        o0.x = as_u32(__builtin_elementwise_fma(as_h2(p.p0) - blo, d0, m0));
-        o0.y = as_u32(__builtin_elementwise_fma(as_h2(p.p1) - bhi, d0, m0));
-        o0.z = as_u32(__builtin_elementwise_fma(as_h2(p.p2) - blo, d0, m0));
-        o0.w = as_u32(__builtin_elementwise_fma(as_h2(p.p3) - bhi, d0, m0));
-        o1.x = as_u32(__builtin_elementwise_fma(as_h2(r.p0) - blo, d1, m1));
-        o1.y = as_u32(__builtin_elementwise_fma(as_h2(r.p1) - bhi, d1, m1));
-        o1.z = as_u32(__builtin_elementwise_fma(as_h2(r.p2) - blo, d1, m1));
-        o1.w = as_u32(__builtin_elementwise_fma(as_h2(r.p3) - bhi, d1, m1));
+        const uint2 v = buf_load8(rq, (unit * 64 + lq) * 16 + 8 * h, 0);
+        st.c[j][ci] = make_uint4(v.x, v.y, 0, 0);
       }
     }
-    *(uint4*)(bs + n * kStride + 8 * kq) = o0;
-    *(uint4*)(bs + n * kStride + 32 + 8 * kq) = o1;
+    const uint32_t soff = ((unit * kTileRows + n) * 4 + 2 * h) * 2;
+    st.dd[j] = buf_load4(rd, soff, 0);
+    if (QT == MLQ_Q4_1) st.mm[j] = buf_load4(rm, soff, 0);
   }
 }
 
-template <int QT, bool VEC>
+// Decodes the fragment of block j, k step ks: 8 codes -> fp16 d*q (d*(q-8),
+// d*q+m), one rounding.
+template <int QT>
+__device__ __forceinline__ h8_t decode_w(const WStage<QT>& st, int j, int ks) {
+  const int ci = ks & 1, blk = ks >> 1;
+  const uint32_t dbits = blk ? (st.dd[j] >> 16) : (st.dd[j] & 0xffffu);
+  const h2_t d2 = h2_splat(dbits);
+  uint4 o;
+  if (QT == MLQ_Q8_0) {
+    const uint4 c = st.c[j][ci];
+    const uint32_t w0 = blk ? c.z : c.x, w1 = blk ? c.w : c.y;
+    const h2_t b = {(_Float16)1152.0f, (_Float16)1152.0f};
+    uint32_t p0, p1, p2, p3;
+    q8_pairs(w0, p0, p1);
+    q8_pairs(w1, p2, p3);
+    o.x = as_u32((as_h2(p0) - b) * d2);
+    o.y = as_u32((as_h2(p1) - b) * d2);
+    o.z = as_u32((as_h2(p2) - b) * d2);
+    o.w = as_u32((as_h2(p3) - b) * d2);
+  } else {
+    const uint32_t w = blk ? st.c[j][ci].y : st.c[j][ci].x;
+    const float lo = QT == MLQ_Q4_0 ? 1032.0f : 1024.0f;
+    const float hi = QT == MLQ_Q4_0 ? 72.0f : 64.0f;
+    const h2_t blo = {(_Float16)lo, (_Float16)lo};
+    const h2_t bhi = {(_Float16)hi, (_Float16)hi};
+    const Q4Pairs p = q4_pairs(w);
+    if (QT == MLQ_Q4_0) {
+      o.x = as_u32((as_h2(p.p0) - blo) * d2);
+      o.y = as_u32((as_h2(p.p1) - bhi) * d2);
+      o.z = as_u32((as_h2(p.p2) - blo) * d2);
+      o.w = as_u32((as_h2(p.p3) - bhi) * d2);
+    } else {
+      const uint32_t mbits = blk ? (st.mm[j] >> 16) : (st.mm[j] & 0xffffu);
+      const h2_t m2 = h2_splat(mbits);
+      o.x = as_u32(__builtin_elementwise_fma(as_h2(p.p0) - blo, d2, m2));
+      o.y = as_u32(__builtin_elementwise_fma(as_h2(p.p1) - bhi, d2, m2));
+      o.z = as_u32(__builtin_elementwise_fma(as_h2(p.p2) - blo, d2, m2));
+      o.w = as_u32(__builtin_elementwise_fma(as_h2(p.p3) - bhi, d2, m2));
+    }
+  }
+  return __builtin_bit_cast(h8_t, o);
+}
+
+template <int QT, int XM>
 __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
   __shared__ __align__(16) _Float16 as_buf[2][kBM * kStride];
-  __shared__ __align__(16) _Float16 bs_buf[2][kBN * kStride];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -213,8 +251,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
   const int tile0 = ntile * kTiles;  // first W row tile
 
   // buffer ranges: rows past m / tiles past nt read as zero
-  const rsrc_t rx = make_rsrc(a.x + (size_t)m0 * a.k,
-                              (uint32_t)((size_t)min(kBM, a.m - m0) * a.k * 4));
+  const int rows = min(kBM, a.m - m0);
+  const rsrc_t rx = XM == kXF16
+      ? make_rsrc(a.xh + (size_t)m0 * a.kp, (uint32_t)((size_t)rows * a.kp * 2))
+      : make_rsrc(a.x + (size_t)m0 * a.k, (uint32_t)((size_t)rows * a.k * 4));
   const int tiles = min(kTiles, a.nt - tile0);
   const uint32_t qbytes = (uint32_t)tiles * a.g * (QT == MLQ_Q8_0 ? 2048u : 1024u);
   const rsrc_t rq = make_rsrc(a.qs + (size_t)tile0 * a.g * (QT == MLQ_Q8_0 ? 2048 : 1024), qbytes);
@@ -231,52 +271,58 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   const int stages = a.g * 2;
-  // Two register stages in flight: stage s+2 is requested while stage s runs
-  // on the MFMAs and stage s+1 (requested one stage earlier) is converted
-  // into LDS, so each load has two stages of work to arrive.
-  Stage<QT> st[2];
-  load_stage<QT, VEC>(a, st[0], rx, rq, rd, rm, 0, tid);
-  if (stages > 1) load_stage<QT, VEC>(a, st[1], rx, rq, rd, rm, 1, tid);
-  store_stage<QT>(a, st[0], as_buf[0], bs_buf[0], 0, tid);
+  // Register ring of two stages: stage s+2 is requested while stage s runs
+  // on the MFMAs and stage s+1's activations are converted into LDS.
+  XStage xs[2];
+  WStage<QT> ws[2];
+  load_x<XM>(a, xs[0], rx, 0, tid);
+  load_w<QT>(a, ws[0], rq, rd, rm, 0, lane, wn);
+  if (stages > 1) {
+    load_x<XM>(a, xs[1], rx, 1, tid);
+    load_w<QT>(a, ws[1], rq, rd, rm, 1, lane, wn);
+  }
+  store_x<XM>(a, xs[0], as_buf[0], 0, tid);
   __syncthreads();
 
   // fragment rows of this lane: MFMA operand row/col = lane % 32, k octet
   // = lane / 32
   const int fr = lane & 31, fk = 8 * (lane >> 5);
-  auto mfma_stage = [&](int cur) {
+  // One stage: decode this stage's weight fragments (freeing its register
+  // slot), request stage s+2 into that slot, run the MFMAs, convert stage
+  // s+1's activations into the other LDS buffer.
+  auto step = [&](int s, XStage& xnext, WStage<QT>& wcur, XStage& xafter) {
+    const int cur = s & 1;
+    h8_t bf[kBK / 16][2];
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[ks][j] = decode_w<QT>(wcur, j, ks);
+    if (s + 2 < stages) {
+      load_x<XM>(a, xafter, rx, s + 2, tid);
+      load_w<QT>(a, wcur, rq, rd, rm, s + 2, lane, wn);
+    }
     const _Float16* as = as_buf[cur];
-    const _Float16* bs = bs_buf[cur];
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      h8_t af[2], bf[2];
+      h8_t af[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
         af[i] = *(const h8_t*)(as + (64 * wm + 32 * i + fr) * kStride + 16 * ks + fk);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *(const h8_t*)(bs + (64 * wn + 32 * j + fr) * kStride + 16 * ks + fk);
-#pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[ks][j], acc[i][j], 0, 0, 0);
     }
-  };
-  // one stage: register buffer `rb` holds stage s+1 on entry and receives
-  // stage s+2
-  auto step = [&](int s, Stage<QT>& next, Stage<QT>& after) {
-    const int cur = s & 1;
-    if (s + 2 < stages) load_stage<QT, VEC>(a, after, rx, rq, rd, rm, s + 2, tid);
-    mfma_stage(cur);
-    if (s + 1 < stages) store_stage<QT>(a, next, as_buf[cur ^ 1], bs_buf[cur ^ 1], s + 1, tid);
+    if (s + 1 < stages) store_x<XM>(a, xnext, as_buf[cur ^ 1], s + 1, tid);
     __syncthreads();
   };
   int s = 0;
   for (; s + 1 < stages; s += 2) {
-    step(s, st[1], st[0]);
-    step(s + 1, st[0], st[1]);
+    step(s, xs[1], ws[0], xs[0]);
+    step(s + 1, xs[0], ws[1], xs[1]);
   }
-  if (s < stages) step(s, st[1], st[0]);
+  if (s < stages) step(s, xs[1], ws[0], xs[0]);
 
   // epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each
   // 32x32 block
@@ -295,44 +341,96 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
   }
 }
 
+// x fp32 [m][k] -> fp16 [m][kp], zero for k <= col < kp. One thread per 8
+// output halves (one 16-byte store).
+__global__ __launch_bounds__(256) void x_to_f16_kernel(const float* x,
+                                                       _Float16* xh, int m,
+                                                       int k, int kp) {
+  const int per_row = kp / 8;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)m * per_row) return;
+  const int r = (int)(idx / per_row), c0 = (int)(idx % per_row) * 8;
+  const float* xr = x + (size_t)r * k;
+  float v[8];
+  if ((k & 3) == 0 && c0 + 8 <= k) {
+    const float4 lo = *(const float4*)(xr + c0);
+    const float4 hi = *(const float4*)(xr + c0 + 4);
+    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = c0 + e < k ? xr[c0 + e] : 0.0f;
+  }
+  uint4 o;
+  o.x = pack_h2(v[0], v[1]);
+  o.y = pack_h2(v[2], v[3]);
+  o.z = pack_h2(v[4], v[5]);
+  o.w = pack_h2(v[6], v[7]);
+  *(uint4*)(xh + (size_t)r * kp + c0) = o;
+}
+
+template <int QT>
+hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
+  const unsigned grid = (unsigned)(a.mtiles * a.ntiles);
+  switch (xm) {
+    case kXF32Vec: gemm_kernel<QT, kXF32Vec><<<grid, kThreads, 0, stream>>>(a); break;
+    case kXF32Scalar: gemm_kernel<QT, kXF32Scalar><<<grid, kThreads, 0, stream>>>(a); break;
+    default: gemm_kernel<QT, kXF16><<<grid, kThreads, 0, stream>>>(a); break;
+  }
+  return hipGetLastError();
+}
+
+// Row stride (halves) of the fp16 activation copy.
+int f16_row_stride(int k) { return (k + kBK - 1) / kBK * kBK; }
+
 }  // namespace
+
+size_t gemm_workspace_bytes(int m, int k) {
+  return (size_t)m * f16_row_stride(k) * 2;
+}
 
 hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream) {
+  return launch_gemm_ws(w, x, y, m, nullptr, 0, stream);
+}
+
+hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
+                          void* ws, size_t ws_bytes, hipStream_t stream) {
   const Geometry geo = geometry(w.n, w.k);
   GemmArgs a;
   a.qs = (const uint8_t*)w.base + w.qs_off;
   a.d = (const uint8_t*)w.base + w.d_off;
   a.mn = w.type == MLQ_Q4_1 ? (const uint8_t*)w.base + w.m_off : nullptr;
   a.x = x;
+  a.xh = nullptr;
   a.y = y;
   a.m = m;
   a.n = w.n;
   a.k = w.k;
   a.g = geo.g;
   a.nt = geo.nt;
+  a.kp = f16_row_stride(w.k);
   a.mtiles = (m + kBM - 1) / kBM;
   a.ntiles = (geo.nt + kTiles - 1) / kTiles;
   // every activation row offset of a workgroup must fit a 32-bit buffer
   // offset
   if ((size_t)kBM * (size_t)w.k * 4 >= (1ull << 31)) return hipErrorInvalidValue;
-  const unsigned grid = (unsigned)(a.mtiles * a.ntiles);
-  const bool vec = (w.k & 3) == 0;
-  switch (w.type) {
-    case MLQ_Q8_0:
-      if (vec) gemm_kernel<MLQ_Q8_0, true><<<grid, kThreads, 0, stream>>>(a);
-      else gemm_kernel<MLQ_Q8_0, false><<<grid, kThreads, 0, stream>>>(a);
-      break;
-    case MLQ_Q4_0:
-      if (vec) gemm_kernel<MLQ_Q4_0, true><<<grid, kThreads, 0, stream>>>(a);
-      else gemm_kernel<MLQ_Q4_0, false><<<grid, kThreads, 0, stream>>>(a);
-      break;
-    default:
-      if (vec) gemm_kernel<MLQ_Q4_1, true><<<grid, kThreads, 0, stream>>>(a);
-      else gemm_kernel<MLQ_Q4_1, false><<<grid, kThreads, 0, stream>>>(a);
-      break;
+  int xm = (w.k & 3) == 0 ? kXF32Vec : kXF32Scalar;
+  if (ws != nullptr && ws_bytes >= gemm_workspace_bytes(m, w.k)) {
+    // one pass over x: fp16 copy, row stride kp, zero tail
+    a.xh = (_Float16*)ws;
+    const size_t items = (size_t)m * (a.kp / 8);
+    x_to_f16_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(
+        x, (_Float16*)ws, m, w.k, a.kp);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    xm = kXF16;
   }
-  return hipGetLastError();
+  switch (w.type) {
+    case MLQ_Q8_0: return launch_typed<MLQ_Q8_0>(a, xm, stream);
+    case MLQ_Q4_0: return launch_typed<MLQ_Q4_0>(a, xm, stream);
+    default: return launch_typed<MLQ_Q4_1>(a, xm, stream);
+  }
 }
 
 }  // namespace mlq

@@ -26,8 +26,12 @@ int gemv_max_k(int type, int m);
 // Split override (0 = automatic); validated by the caller.
 void set_gemv_split(int split);
 
-// gemm_mfma.hip: any m >= 1.
+// gemm_mfma.hip: any m >= 1. The _ws form converts x to fp16 into `ws`
+// first when ws_bytes >= gemm_workspace_bytes(m, k) (else reads fp32 x).
 hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream);
+hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
+                          void* ws, size_t ws_bytes, hipStream_t stream);
+size_t gemm_workspace_bytes(int m, int k);
 
 }  // namespace mlq

@@ -211,6 +211,34 @@ def test_linear_1d_input_and_aos_path(pkg, oracle, cuda, qtype):
     assert tolerance_ok(y_tiled, ref, x[None], k).all()
 
 
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("m,n,k", [(9, 40, 200), (130, 70, 300), (64, 256, 4096),
+                                   (300, 100, 1001)])
+def test_gemm_workspace_path_matches_direct(pkg, cuda, qtype, m, n, k):
+    """mlq_linear_ws (fp16 copy of x made by a pre-pass) and the direct GEMM
+    (x converted inside) round x to fp16 identically, so they must agree bit
+    for bit; the workspace contract is enforced."""
+    torch = _torch()
+    _print_case(test="gemm_ws", qtype=qtype, m=m, n=n, k=k)
+    blocks = make_blocks(qtype, n, k, seed=m + n + k)
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    xd = _dev(make_x(m, k, seed=k), cuda)
+    need = pkg.workspace_bytes(tw, m)
+    assert need >= m * k * 2
+    ws = torch.empty(need, dtype=torch.uint8, device=cuda)
+    got_ws = pkg.linear(tw, xd, workspace=ws).cpu().numpy()
+    got_direct = pkg.linear(tw, xd, path=pkg.PATH_MFMA).cpu().numpy()
+    assert np.array_equal(got_ws, got_direct)
+    with pytest.raises(pkg.MLQError) as e:
+        pkg.linear(tw, xd, workspace=ws[: need - 1])
+    assert e.value.status == -4
+    big = torch.empty(need + 256, dtype=torch.uint8, device=cuda)
+    with pytest.raises(pkg.MLQError) as e:
+        pkg.linear(tw, xd, workspace=big[16:])  # large enough, misaligned
+    assert e.value.status == -1
+    assert pkg.workspace_bytes(tw, 1) == 0  # decode GEMV needs none
+
+
 def test_bias_kernel(pkg, cuda):
     torch = _torch()
     y = torch.arange(12, dtype=torch.float32, device=cuda).reshape(3, 4)
