@@ -223,6 +223,13 @@ int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
   if (workspace == nullptr || workspace_bytes < need)
     return MLQ_ERR_BUFFER_TOO_SMALL;
   if (((uintptr_t)workspace & 255u) != 0) return MLQ_ERR_INVALID_ARG;
+  if (m <= kSkinnyMaxRows) {
+    // batched decode: fp16 copy of x, then the skinny GEMM
+    _Float16* xh = (_Float16*)workspace;
+    rc = hip_status(launch_x_to_f16(x, xh, m, w->k, s));
+    if (rc != MLQ_OK) return rc;
+    return hip_status(launch_skinny(*w, xh, f16_row_stride(w->k), y, m, s));
+  }
   return hip_status(launch_gemm_ws(*w, x, y, m, workspace, workspace_bytes, s));
 }
 

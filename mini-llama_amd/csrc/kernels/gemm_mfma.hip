@@ -380,13 +380,23 @@ hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Row stride (halves) of the fp16 activation copy.
-int f16_row_stride(int k) { return (k + kBK - 1) / kBK * kBK; }
-
 }  // namespace
+
+// Row stride (halves) of the fp16 activation copy: whole 128-k groups, so
+// every stage (GEMM) and group (skinny GEMM) of a row stays inside it.
+int f16_row_stride(int k) { return (k + kGroupK - 1) / kGroupK * kGroupK; }
 
 size_t gemm_workspace_bytes(int m, int k) {
   return (size_t)m * f16_row_stride(k) * 2;
+}
+
+hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,
+                           hipStream_t stream) {
+  const int kp = f16_row_stride(k);
+  const size_t items = (size_t)m * (kp / 8);
+  x_to_f16_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(x, xh, m,
+                                                                        k, kp);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
@@ -419,10 +429,7 @@ hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
   if (ws != nullptr && ws_bytes >= gemm_workspace_bytes(m, w.k)) {
     // one pass over x: fp16 copy, row stride kp, zero tail
     a.xh = (_Float16*)ws;
-    const size_t items = (size_t)m * (a.kp / 8);
-    x_to_f16_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(
-        x, (_Float16*)ws, m, w.k, a.kp);
-    const hipError_t e = hipGetLastError();
+    const hipError_t e = launch_x_to_f16(x, (_Float16*)ws, m, w.k, stream);
     if (e != hipSuccess) return e;
     xm = kXF16;
   }

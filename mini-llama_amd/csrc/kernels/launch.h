@@ -33,5 +33,14 @@ hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
 hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
                           void* ws, size_t ws_bytes, hipStream_t stream);
 size_t gemm_workspace_bytes(int m, int k);
+// fp16 copy of x [m][k] into xh [m][f16_row_stride(k)] (zero past k).
+int f16_row_stride(int k);
+hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,
+                           hipStream_t stream);
+
+// skinny.hip: 9..64 rows of x from its fp16 copy (row stride kp).
+constexpr int kSkinnyMaxRows = 64;
+hipError_t launch_skinny(const mlq_weight& w, const _Float16* xh, int kp,
+                         float* y, int m, hipStream_t stream);
 
 }  // namespace mlq
