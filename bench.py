@@ -152,25 +152,39 @@ def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed, eager=False):
     return out
 
 
-def bench_sweep(pkg, torch, steps, warmup):
+SWEEP_SHAPES = [("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584),
+                ("o", 3584, 3584), ("gate", 18944, 3584), ("up", 18944, 3584),
+                ("down", 3584, 18944)]
+
+
+def bench_sweep(pkg, torch, steps, warmup, fused):
     """28 layers x {q,k,v,o,gate,up,down} q4_0 GEMVs (hidden 3584, FFN 18944,
-    GQA kv 512), M = 1, one fixed x per shape, one graph = one decode step."""
+    GQA kv 512), M = 1, one fixed x per input size, one graph = one decode
+    step. fused=True uploads q|k|v and gate|up as concatenated weights (each
+    pair/triple shares its input), so a layer is 4 launches instead of 7;
+    the bytes and flops are the same."""
     import mini_llama_amd.synth as synth
-    shapes = [("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584),
-              ("o", 3584, 3584), ("gate", 18944, 3584), ("up", 18944, 3584),
-              ("down", 3584, 18944)]
     xs = {kk: torch.from_numpy(synth.make_x(1, kk, 900 + kk)[0]).to("cuda")
           for kk in (3584, 18944)}
-    ys = {nn: torch.empty(nn, dtype=torch.float32, device="cuda")
-          for nn in (512, 3584, 18944)}
-    layers = []
-    log("sweep: uploading 28 layers")
+    log(f"sweep ({'fused' if fused else '196 launches'}): uploading 28 layers")
+    calls = []
     for layer in range(28):
-        layers.append([pkg.upload("q4_0", synth.make_blocks("q4_0", n, k,
-                                                             5000 + 10 * layer + i),
-                                  n, k, device="cuda")
-                       for i, (_, n, k) in enumerate(shapes)])
-    calls = [(w, xs[w.k], ys[w.n]) for lw in layers for w in lw]
+        blk = {name: (synth.make_blocks("q4_0", n, k, 5000 + 10 * layer + i), n, k)
+               for i, (name, n, k) in enumerate(SWEEP_SHAPES)}
+        if fused:
+            groups = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
+        else:
+            groups = [[name] for name, _, _ in SWEEP_SHAPES]
+        for g in groups:
+            k = blk[g[0]][2]
+            if len(g) == 1:
+                w = pkg.upload("q4_0", blk[g[0]][0], blk[g[0]][1], k, device="cuda")
+            else:
+                w, _ = pkg.upload_concat("q4_0", [(blk[nm][0], blk[nm][1]) for nm in g],
+                                         k, device="cuda")
+            y = torch.empty(w.n, dtype=torch.float32, device="cuda")
+            calls.append((w, xs[k], y))
+    del blk
 
     def step(_):
         for w, x, y in calls:
@@ -178,12 +192,13 @@ def bench_sweep(pkg, torch, steps, warmup):
 
     steps = max(1, steps)
     sec = time_graph(torch, step, steps, warmup) / steps
-    total = sum(alg_bytes("q4_0", 1, w.n, w.k) for w, _, _ in calls)
-    flops = sum(alg_flops(1, w.n, w.k) for w, _, _ in calls)
-    del layers, calls
+    total = sum(alg_bytes("q4_0", 1, n, k) for _ in range(28) for _, n, k in SWEEP_SHAPES)
+    flops = sum(alg_flops(1, n, k) for _ in range(28) for _, n, k in SWEEP_SHAPES)
+    launches = len(calls)
+    del calls
     torch.cuda.empty_cache()
-    return {"gemvs": 196, "us_per_step": sec * 1e6, "gbs": total / sec / 1e9,
-            "bytes": total, "tflops": flops / sec / 1e12}
+    return {"gemvs": 196, "launches": launches, "us_per_step": sec * 1e6,
+            "gbs": total / sec / 1e9, "bytes": total, "tflops": flops / sec / 1e12}
 
 
 def cpu_baseline(qtype, n, k, budget_s=10.0):
@@ -294,10 +309,11 @@ def main():
             extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
                            for kk, v in r.items()}
             extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
-        sw = bench_sweep(pkg, torch, max(1, args.steps // 100), 1)
-        sw["frac_hbm"] = round(sw["gbs"] / HBM_PEAK_GBS, 4)
-        extra["sweep"] = {kk: (round(v, 3) if isinstance(v, float) else v)
-                          for kk, v in sw.items()}
+        for fused in (False, True):
+            sw = bench_sweep(pkg, torch, max(1, args.steps // 100), 1, fused)
+            sw["frac_hbm"] = round(sw["gbs"] / HBM_PEAK_GBS, 4)
+            extra["sweep_fused" if fused else "sweep"] = {
+                kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in sw.items()}
         result["configs"] = extra
     if not args.no_cpu:
         log("cpu baseline")

@@ -179,6 +179,18 @@ def upload(qtype: str, blocks: np.ndarray, n: int, k: int,
     return TiledWeight(qtype, n, k, buf, layout)
 
 
+def upload_concat(qtype: str, parts, k: int, device: str = "cuda"):
+    """Several weights that share one input (q|k|v, gate|up) as one tiled
+    weight: their rows are concatenated, so one launch computes all of them.
+    `parts` is a list of (blocks, n). Returns (TiledWeight, row offsets);
+    output rows [off[i], off[i+1]) belong to part i."""
+    blocks = np.concatenate([np.ascontiguousarray(b).view(np.uint8).reshape(-1)
+                             for b, _ in parts])
+    ns = [int(n) for _, n in parts]
+    offsets = np.concatenate([[0], np.cumsum(ns)]).tolist()
+    return upload(qtype, blocks, offsets[-1], k, device=device), offsets
+
+
 def upload_aos(blocks: np.ndarray, device: str = "cuda"):
     """Raw GGUF blocks to device memory unchanged (what the reference uploads)."""
     import torch

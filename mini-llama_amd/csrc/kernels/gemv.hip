@@ -20,9 +20,10 @@
 //    wave's private LDS slice, which therefore overlaps the weight fetch.
 //    The group loop has no data-dependent branch: a shorter last slice
 //    processes zero groups (zero scales, zero activations). Slices longer
-//    than 8 groups run a ring of 8 slots instead, each refilled 8 groups
-//    ahead as soon as its codes are decoded (refills past the slice read
-//    zeros, so they need no branch either).
+//    than the register budget run a ring of GW slots instead (GW chosen to
+//    pad the slice least), each refilled GW groups ahead as soon as its
+//    codes are decoded (refills past the slice read zeros, so they need no
+//    branch either).
 //  - Lane L = n + 16*kq holds quarter kq of the group's 4 blocks of row n,
 //    which is the B operand of v_mfma_f32_16x16x32_f16 for one block. Codes
 //    are decoded EXACTLY to fp16 (q-8, q, or q): one AND-OR places a code in
@@ -397,27 +398,42 @@ int split_override() {
 struct Plan {
   int split, gw;
   int depth;  // GW: groups in flight per wave (1..8)
-  bool ring;  // slices longer than 8 groups: ring of 8 slots
+  bool ring;  // slices longer than max_depth groups: ring of `depth` slots
   int padded; // groups staged per wave (gw, or whole ring passes)
   size_t wave_lds, lds;
 };
 
 // Groups in flight per wave without spilling (VGPR budget of a 1024-thread
-// workgroup): every group of the slice when gw <= max_depth, else a ring of
-// ring_depth slots. q4_1 carries mins and block sums per group.
+// workgroup): every group of the slice when gw <= max_depth, else a ring.
+// q4_1 carries mins and block sums per group, so its budgets are smaller.
 constexpr int kMaxDepth = 8;
 int max_depth(int type, int m) {
   if (type == MLQ_Q4_1) return m == 1 ? 6 : 3;
   return kMaxDepth;
 }
-constexpr int ring_depth(int type, int mr) {
-  return type == MLQ_Q4_1 ? (mr == 1 ? 4 : 2) : 8;
+// Ring depths that compile without spills, per type and row class.
+int ring_depth_lo(int type, int m) { return type == MLQ_Q4_1 ? (m == 1 ? 3 : 2) : 4; }
+int ring_depth_hi(int type, int m) { return type == MLQ_Q4_1 ? (m == 1 ? 4 : 2) : 8; }
+
+// Ring depth for a slice of gw groups: the one that pads the slice least to
+// whole passes (padded groups cost decode and MFMA work on zeros), the
+// deeper one on ties.
+int ring_depth(int type, int m, int gw) {
+  int best = ring_depth_hi(type, m), best_pad = 1 << 30;
+  for (int d = ring_depth_hi(type, m); d >= ring_depth_lo(type, m); --d) {
+    const int pad = (gw + d - 1) / d * d - gw;
+    if (pad < best_pad) {
+      best = d;
+      best_pad = pad;
+    }
+  }
+  return best;
 }
 
 // Groups a wave of `gw` processes (and stages activations for).
 int padded_groups(int type, int m, int gw) {
   if (gw <= max_depth(type, m)) return gw;
-  const int rd = ring_depth(type, m == 1 ? 1 : kGemvMaxRows);
+  const int rd = ring_depth(type, m, gw);
   return (gw + rd - 1) / rd * rd;
 }
 
@@ -433,14 +449,20 @@ Plan make_plan(int type, int m, const Geometry& geo) {
   Plan p;
   const int env_split = split_override();
   // Default split: enough waves for the whole grid to be resident at about
-  // 16 waves per CU, but at least two groups per wave.
+  // 16 waves per CU (keeping at least two groups per wave), and short
+  // enough slices that every group of a slice is in flight at once (no
+  // ring) when a workgroup of 16 waves allows it.
   int split = 1;
   if (env_split >= 1 && env_split <= kMaxSplit && (env_split & (env_split - 1)) == 0) {
     split = env_split;
   } else {
-    while (split < kMaxSplit && geo.nt * split < kTargetWaves &&
-           (geo.g + 2 * split - 1) / (2 * split) >= 2)
+    while (split < kMaxSplit && 2 * split <= geo.g) {
+      const bool more_waves = geo.nt * split < kTargetWaves &&
+                              (geo.g + 2 * split - 1) / (2 * split) >= 2;
+      const bool shorter = (geo.g + split - 1) / split > max_depth(type, m);
+      if (!more_waves && !shorter) break;
       split *= 2;
+    }
   }
   split = std::min(split, std::max(1, geo.g));
   // Each wave stages its own K slice: widen the split until they fit in LDS.
@@ -460,7 +482,7 @@ Plan make_plan(int type, int m, const Geometry& geo) {
   // Every group of the slice in flight at once (depth = gw) when it fits,
   // otherwise the ring.
   p.ring = p.gw > max_depth(type, m);
-  p.depth = p.ring ? ring_depth(type, m == 1 ? 1 : kGemvMaxRows) : p.gw;
+  p.depth = p.ring ? ring_depth(type, m, p.gw) : p.gw;
   p.padded = padded_groups(type, m, p.gw);
   return p;
 }
@@ -482,7 +504,22 @@ hipError_t launch_typed(const GemvArgs& a, size_t lds, hipStream_t stream) {
 
 template <int QT, int MR>
 hipError_t launch_depth(const GemvArgs& a, const Plan& p, hipStream_t stream) {
-  if (p.ring) return launch_typed<QT, MR, ring_depth(QT, MR), true>(a, p.lds, stream);
+  if (p.ring) {
+    if constexpr (QT == MLQ_Q4_1 && MR > 1) {
+      return launch_typed<QT, MR, 2, true>(a, p.lds, stream);
+    } else if constexpr (QT == MLQ_Q4_1) {
+      if (p.depth == 3) return launch_typed<QT, MR, 3, true>(a, p.lds, stream);
+      return launch_typed<QT, MR, 4, true>(a, p.lds, stream);
+    } else {
+    switch (p.depth) {
+      case 4: return launch_typed<QT, MR, 4, true>(a, p.lds, stream);
+      case 5: return launch_typed<QT, MR, 5, true>(a, p.lds, stream);
+      case 6: return launch_typed<QT, MR, 6, true>(a, p.lds, stream);
+      case 7: return launch_typed<QT, MR, 7, true>(a, p.lds, stream);
+      default: return launch_typed<QT, MR, 8, true>(a, p.lds, stream);
+    }
+    }
+  }
   // (depths above max_depth(QT, m) are never planned)
   switch (p.depth) {
     case 1: return launch_typed<QT, MR, 1, false>(a, p.lds, stream);

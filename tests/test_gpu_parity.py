@@ -248,6 +248,22 @@ def test_gemm_workspace_path_matches_direct(pkg, cuda, qtype, m, n, k):
     assert pkg.workspace_bytes(tw, 1) == 0  # decode GEMV needs none
 
 
+@pytest.mark.parametrize("m", [1, 3, 16])
+def test_concatenated_weights_match_separate(pkg, oracle, cuda, m):
+    """q|k|v-style fusion: one tiled weight holding several weights' rows
+    (shared input) gives each part's outputs in its row range."""
+    k = 640
+    parts = [(make_blocks("q4_0", n, k, seed=n), n) for n in (48, 16, 21)]
+    tw, off = pkg.upload_concat("q4_0", parts, k, device=cuda)
+    x = make_x(m, k, seed=5)
+    y = pkg.linear(tw, _dev(x if m > 1 else x[0], cuda)).cpu().numpy()
+    y = np.atleast_2d(y)
+    for i, (blocks, n) in enumerate(parts):
+        ref = oracle.linear(x, blocks, (n, k), "q4_0")
+        got = y[:, off[i]:off[i + 1]]
+        assert tolerance_ok(got, ref, x, k).all(), (i, error_report(got, ref, x, k))
+
+
 def test_bias_kernel(pkg, cuda):
     torch = _torch()
     y = torch.arange(12, dtype=torch.float32, device=cuda).reshape(3, 4)
