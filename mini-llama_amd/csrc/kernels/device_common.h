@@ -91,6 +91,16 @@ __device__ __forceinline__ uint4 buf_load16(rsrc_t r, uint32_t voff,
   return __builtin_bit_cast(
       uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
+// Cache-policy bits of a buffer load: NT marks data read once (weight lines
+// streamed by the decode kernels), so the caches do not keep it at the
+// expense of reused data (activations). Measured 3-9% faster GEMVs on MI355X.
+constexpr int kLoadNonTemporal = 2;
+__device__ __forceinline__ uint4 buf_load16_stream(rsrc_t r, uint32_t voff,
+                                                   uint32_t soff) {
+  return __builtin_bit_cast(
+      uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff,
+                                                   kLoadNonTemporal));
+}
 __device__ __forceinline__ uint2 buf_load8(rsrc_t r, uint32_t voff,
                                            uint32_t soff) {
   return __builtin_bit_cast(

@@ -47,7 +47,7 @@ namespace mlq {
 namespace {
 
 constexpr int kMaxSplit = 16;       // waves per workgroup (one tile)
-constexpr int kTargetWaves = 4096;  // ~16 resident waves per CU on 256 CUs
+constexpr int kTargetWaves = 8192;  // ~32 waves per CU on 256 CUs (measured best)
 constexpr int kRowPadHalves = 32;   // 64 B: consecutive LDS rows hit other banks
 constexpr int kUnitScaleBytes = kTileRows * kGroupBlocks * 2;  // 128 B
 constexpr int kXRegs = 4;           // float4 activation loads held per lane
@@ -102,8 +102,8 @@ template <int QT>
 __device__ __forceinline__ void load_group(const WaveRsrc& r, Slot<QT>& s,
                                            int j, uint32_t qoff, uint32_t soff) {
   const uint32_t qb = (uint32_t)j * unit_quant_bytes<QT>();
-  s.q = buf_load16(r.q, qoff, qb);
-  if (QT == MLQ_Q8_0) s.q2 = buf_load16(r.q, qoff, qb + 1024u);
+  s.q = buf_load16_stream(r.q, qoff, qb);
+  if (QT == MLQ_Q8_0) s.q2 = buf_load16_stream(r.q, qoff, qb + 1024u);
   s.d = buf_load8(r.d, soff, (uint32_t)j * kUnitScaleBytes);
   if (QT == MLQ_Q4_1) s.m = buf_load8(r.m, soff, (uint32_t)j * kUnitScaleBytes);
 }
@@ -448,8 +448,8 @@ size_t wave_lds_bytes(int type, int m, int gw) {
 Plan make_plan(int type, int m, const Geometry& geo) {
   Plan p;
   const int env_split = split_override();
-  // Default split: enough waves for the whole grid to be resident at about
-  // 16 waves per CU (keeping at least two groups per wave), and short
+  // Default split: about 32 waves per CU (keeping at least two groups per
+  // wave), and short
   // enough slices that every group of a slice is in flight at once (no
   // ring) when a workgroup of 16 waves allows it.
   int split = 1;

@@ -52,10 +52,10 @@ __device__ __forceinline__ void load_group(const SkinnyArgs& a, Group<QT, MB>& g
                                            rsrc_t rx, int j, int lane) {
   const uint32_t unit = (uint32_t)j;  // relative to the wave's first unit
   if (QT == MLQ_Q8_0) {
-    gr.q = buf_load16(rq, ((unit * 2) * 64 + lane) * 16, 0);
-    gr.q2 = buf_load16(rq, ((unit * 2 + 1) * 64 + lane) * 16, 0);
+    gr.q = buf_load16_stream(rq, ((unit * 2) * 64 + lane) * 16, 0);
+    gr.q2 = buf_load16_stream(rq, ((unit * 2 + 1) * 64 + lane) * 16, 0);
   } else {
-    gr.q = buf_load16(rq, (unit * 64 + lane) * 16, 0);
+    gr.q = buf_load16_stream(rq, (unit * 64 + lane) * 16, 0);
   }
   const uint32_t soff = (unit * kTileRows + (lane & 15)) * 8;
   gr.d = buf_load8(rd, soff, 0);
