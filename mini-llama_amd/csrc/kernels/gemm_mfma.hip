@@ -3,24 +3,28 @@
 // The reference never issues m > 1 on the GPU (src/batch.cc:32-55 loops
 // tokens); its kernels (src/cuda_quant.cu:78-182) re-stream W once per row
 // of x (grid.y = rows). This kernel is a dense contraction instead:
-//  - Workgroup tile 128 (m) x 128 (n), four waves in a 2 x 2 grid, each wave
-//    64 x 64 = 2 x 2 v_mfma_f32_32x32x16_f16 (fp32 accumulate). The 32x32
-//    shape does twice the work per operand register of 16x16x32, which
-//    halves the LDS read traffic per flop.
-//  - K advances in stages of 64 (half of a 128-k group). Activations are
-//    converted fp32 -> fp16 into an LDS slab [row][k] with a 16-byte row pad
-//    (every A fragment is one conflict-free ds_read_b128).
-//  - Weights never touch LDS: with 64 x 64 wave tiles, LDS fragment reads
-//    cost as much as the MFMAs themselves on this part (~128 B/clk per CU),
-//    so each wave loads its own B fragments straight from the tiled layout
-//    (two 16-byte chunks per lane cover a stage's four k steps) and decodes
-//    them in registers (codes exact, then scaled by d in fp16: one
-//    rounding, like d*q rounded to fp16). Halves LDS traffic per flop.
-//  - A register ring of two stages: stage s+2 is requested while stage s
-//    runs on the MFMAs and stage s+1's activations go into the other LDS
-//    buffer; one barrier per stage.
-//  - Workgroups are numbered XCD-major: the four m-tiles of one weight
-//    column block run on the same XCD and share its L2.
+//  - Workgroup tile 128 (m) x 256 (n), four waves side by side in n, each
+//    wave 128 x 64 = 4 x 2 v_mfma_f32_32x32x16_f16 (fp32 accumulate). Every
+//    weight is decoded by exactly one wave of the workgroup (the VALU decode
+//    is the scarce resource next to the MFMAs), and every decoded fragment
+//    feeds four MFMAs.
+//  - K advances in stages of 64 (half of a 128-k group). Activations go
+//    through LDS slabs [row][k] with a 16-byte row pad (every A fragment is
+//    one conflict-free ds_read_b128); all four waves read the whole slab.
+//  - Weights never touch LDS: each wave loads its own B fragments straight
+//    from the tiled layout (two 16-byte chunks per lane cover a stage's four
+//    k steps) and decodes them in registers (codes exact, then scaled by d
+//    in fp16: one rounding, like d*q rounded to fp16).
+//  - Software pipeline, one wave per SIMD: three LDS slabs (stage s reads
+//    slab s%3, x(s+2) is written into slab (s+2)%3, and the first fragments
+//    of stage s+1 are read from slab (s+1)%3 before the stage's barrier),
+//    weights three stages deep in registers, the A fragments and decoded B
+//    fragments of k step t+1 prepared while the MFMAs of step t run. Global
+//    loads, LDS reads and LDS writes are spread one at a time between the
+//    MFMAs (sched_group_barrier), so neither the texture unit nor the LDS
+//    sees a burst from all four waves at once.
+//  - Workgroups are numbered XCD-major: the m-tiles of one weight column
+//    block run on the same XCD and share its L2.
 //  - With a workspace, x is first converted once to an fp16 copy
 //    (x_to_f16_kernel): the GEMM then moves half the activation bytes per
 //    stage and does no conversion work. Without one it reads fp32 x.
@@ -37,9 +41,9 @@ namespace mlq {
 namespace {
 
 constexpr int kBM = 128;           // x rows per workgroup
-constexpr int kBN = 128;           // W rows per workgroup (8 row tiles)
+constexpr int kBN = 256;           // W rows per workgroup (16 row tiles)
 constexpr int kBK = 64;            // k per stage
-constexpr int kTiles = kBN / kTileRows;  // 8: wave column block j covers tiles 4wn+2j, +1
+constexpr int kTiles = kBN / kTileRows;  // 16: wave wn, column block j covers tiles 4wn+2j, +1
 constexpr int kThreads = 256;
 constexpr int kStride = kBK + 8;   // halves per LDS row (144 B)
 constexpr int kXcds = 8;
@@ -231,14 +235,16 @@ __device__ __forceinline__ h8_t decode_w(const WStage<QT>& st, int j, int ks) {
   return __builtin_bit_cast(h8_t, o);
 }
 
+template <int N>
+struct Slot { static constexpr int v = N; };
+
 template <int QT, int XM>
-__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
-  __shared__ __align__(16) _Float16 as_buf[2][kBM * kStride];
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs a) {
+  __shared__ __align__(16) _Float16 as_buf[3][kBM * kStride];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wn = tid >> 6;  // wave: W rows 64wn .. 64wn+63 of the tile
 
   // XCD-major numbering: hardware sends workgroup b to XCD b % 8; remap so
   // that each XCD gets a contiguous run of logical ids (m fastest).
@@ -262,79 +268,116 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmArgs a) {
   const rsrc_t rd = make_rsrc(a.d + (size_t)tile0 * a.g * 128, sbytes);
   const rsrc_t rm = QT == MLQ_Q4_1 ? make_rsrc(a.mn + (size_t)tile0 * a.g * 128, sbytes) : rd;
 
-  f16v_t acc[2][2];
+  f16v_t acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int stages = a.g * 2;
-  // Register ring of two stages: stage s+2 is requested while stage s runs
-  // on the MFMAs and stage s+1's activations are converted into LDS.
-  XStage xs[2];
-  WStage<QT> ws[2];
-  load_x<XM>(a, xs[0], rx, 0, tid);
-  load_w<QT>(a, ws[0], rq, rd, rm, 0, lane, wn);
-  if (stages > 1) {
-    load_x<XM>(a, xs[1], rx, 1, tid);
-    load_w<QT>(a, ws[1], rq, rd, rm, 1, lane, wn);
-  }
-  store_x<XM>(a, xs[0], as_buf[0], 0, tid);
-  __syncthreads();
-
+  const int stages = a.g * 2;  // even, >= 2
+  const int last = stages - 1;
   // fragment rows of this lane: MFMA operand row/col = lane % 32, k octet
   // = lane / 32
   const int fr = lane & 31, fk = 8 * (lane >> 5);
-  // One stage: decode this stage's weight fragments (freeing its register
-  // slot), request stage s+2 into that slot, run the MFMAs, convert stage
-  // s+1's activations into the other LDS buffer.
-  auto step = [&](int s, XStage& xnext, WStage<QT>& wcur, XStage& xafter) {
-    const int cur = s & 1;
-    h8_t bf[kBK / 16][2];
+  auto read_a = [&](h8_t (&af)[4], int slab, int ks) {
+    const _Float16* as = as_buf[slab];
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks)
+    for (int i = 0; i < 4; ++i)
+      af[i] = *(const h8_t*)(as + (32 * i + fr) * kStride + 16 * ks + fk);
+  };
+
+  // prologue: slabs 0 and 1 hold x(0), x(1); x(2) in register slot 0;
+  // W(0), W(1) in slots 0 and 1
+  XStage xs[2];
+  WStage<QT> ws[3];
+  load_x<XM>(a, xs[0], rx, 0, tid);
+  load_w<QT>(a, ws[0], rq, rd, rm, 0, lane, wn);
+  load_x<XM>(a, xs[1], rx, 1, tid);
+  load_w<QT>(a, ws[1], rq, rd, rm, 1, lane, wn);
+  store_x<XM>(a, xs[0], as_buf[0], 0, tid);
+  store_x<XM>(a, xs[1], as_buf[1], 1, tid);
+  load_x<XM>(a, xs[0], rx, min(2, last), tid);
+  __syncthreads();
+
+  h8_t af[4], bf[2];
+  read_a(af, 0, 0);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bf[ks][j] = decode_w<QT>(wcur, j, ks);
-    if (s + 2 < stages) {
-      load_x<XM>(a, xafter, rx, s + 2, tid);
-      load_w<QT>(a, wcur, rq, rd, rm, s + 2, lane, wn);
-    }
-    const _Float16* as = as_buf[cur];
+  for (int j = 0; j < 2; ++j) bf[j] = decode_w<QT>(ws[0], j, 0);
+
+  // Stage s; the register slots are compile-time (S = s mod 6): weights of
+  // stage s in slot s%3 (s+1 in flight in (s+1)%3, s+2 requested into
+  // (s+2)%3), x(s+2) in slot s%2 (x(s+3) requested into (s+1)%2). Loads
+  // past the last stage re-read the last one, so the ring never branches.
+  auto step = [&](int s, auto slot) {
+    constexpr int S = decltype(slot)::v;
+    constexpr int WC = S % 3, WN = (S + 1) % 3, WA = (S + 2) % 3;
+    constexpr int XC = S % 2, XA = (S + 1) % 2;
+    constexpr int BC = S % 3, BN = (S + 1) % 3, BA = (S + 2) % 3;
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      h8_t af[2];
+      if (ks == 0) load_x<XM>(a, xs[XA], rx, min(s + 3, last), tid);
+      if (ks == 1) load_w<QT>(a, ws[WA], rq, rd, rm, min(s + 2, last), lane, wn);
+      h8_t an[4], bn[2];
+      if (ks < kBK / 16 - 1) {
+        read_a(an, BC, ks + 1);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *(const h8_t*)(as + (64 * wm + 32 * i + fr) * kStride + 16 * ks + fk);
+        for (int j = 0; j < 2; ++j) bn[j] = decode_w<QT>(ws[WC], j, ks + 1);
+      } else {
+        if (s + 2 < stages) store_x<XM>(a, xs[XC], as_buf[BA], s + 2, tid);
+        read_a(an, BN, 0);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j) bn[j] = decode_w<QT>(ws[WN], j, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[ks][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      // each MFMA followed by four VALU (decode) instructions and at most
+      // one memory instruction: LDS reads of the next k step, global loads
+      // (x in step 0, weights in step 1), the slab store in step 3
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        if (ks == kBK / 16 - 1) {
+          if (q < 4) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+          else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // LDS read
+        } else {
+          if (q % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (ks == 0 && q < 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+          if (ks == 1 && q < 6) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = an[i];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = bn[j];
     }
-    if (s + 1 < stages) store_x<XM>(a, xnext, as_buf[cur ^ 1], s + 1, tid);
     __syncthreads();
   };
   int s = 0;
-  for (; s + 1 < stages; s += 2) {
-    step(s, xs[1], ws[0], xs[0]);
-    step(s + 1, xs[0], ws[1], xs[1]);
+  for (; s + 6 <= stages; s += 6) {
+    step(s, Slot<0>{}); step(s + 1, Slot<1>{}); step(s + 2, Slot<2>{});
+    step(s + 3, Slot<3>{}); step(s + 4, Slot<4>{}); step(s + 5, Slot<5>{});
   }
-  if (s < stages) step(s, xs[1], ws[0], xs[0]);
+  if (s + 2 <= stages) { step(s, Slot<0>{}); step(s + 1, Slot<1>{}); }
+  if (s + 4 <= stages) { step(s + 2, Slot<2>{}); step(s + 3, Slot<3>{}); }
 
   // epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each
   // 32x32 block
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int ncol = tile0 * kTileRows + 64 * wn + 32 * j + fr;
       if (ncol >= a.n) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int mrow = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int mrow = m0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (mrow < a.m) a.y[(size_t)mrow * a.n + ncol] = acc[i][j][r];
       }
     }

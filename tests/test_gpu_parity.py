@@ -294,7 +294,10 @@ def test_validation_errors(pkg, cuda):
 CONFIGS = [("c0", "q8_0", 1, 4096, 4096), ("c1", "q4_0", 1, 18944, 3584),
            ("c2", "q4_1", 1, 4096, 14336), ("c3", "q4_0", 4, 4096, 4096),
            ("c3", "q4_0", 16, 4096, 4096), ("c3", "q4_0", 64, 4096, 4096),
-           ("c4", "q8_0", 512, 11008, 4096)]
+           ("c4", "q8_0", 512, 11008, 4096),
+           # decode-sweep shapes: K = 18944 takes the GEMV refill ring,
+           # N = 37888 is the fused gate|up weight
+           ("down", "q4_0", 1, 3584, 18944), ("gateup", "q4_0", 1, 37888, 3584)]
 
 
 @pytest.mark.parametrize("cfg,qtype,m,n,k", CONFIGS)
