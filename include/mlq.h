@@ -135,8 +135,11 @@ int mlq_linear(const mlq_weight* w, const float* x, float* y, int m,
 
 /* Device workspace bytes mlq_linear_ws needs for m activation rows with
  * weight w (*bytes = 0 when the kernels for that shape need none: the decode
- * GEMV). The prefill GEMM uses it for a one-pass fp16 copy of x, which
- * halves the activation bytes its stages move. */
+ * GEMV). The skinny and prefill GEMMs use it for a one-pass fp16 copy of x,
+ * which halves the activation bytes their stages move; the prefill GEMM
+ * also for fp32 partial outputs when it splits K across workgroups (shapes
+ * with few output tiles). The size depends on the shape, the split-K
+ * override and the device's compute-unit count. */
 int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes);
 
 /* mlq_linear with a caller workspace of at least mlq_linear_workspace(w, m)
@@ -172,6 +175,14 @@ int mlq_linear_path(const mlq_weight* w, const float* x, float* y, int m,
  * flight follows from the slice length. Returns MLQ_ERR_INVALID_ARG for
  * other values. */
 int mlq_set_gemv_split(int split);
+
+/* Prefill GEMM split-K override for tuning and tests (process-wide): the
+ * K range of every output tile is divided over `split` workgroups (capped
+ * at one 128-k group each) whose fp32 partials are summed in split order;
+ * 0 restores the planner. Applies to mlq_linear_ws calls that take the
+ * prefill GEMM (m > 64); query mlq_linear_workspace after changing it.
+ * MLQ_ERR_INVALID_ARG outside 0..64. */
+int mlq_set_gemm_split(int split);
 
 /* Add bias[n] to every row of y[m, n] on the device (the reference adds the
  * bias on the host after download, src/cuda_quant.cu:229-235, 327-329). */

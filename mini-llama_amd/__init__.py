@@ -80,6 +80,7 @@ SIGNATURES = {
     "mlq_linear_ws": ([_WP, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
     "mlq_set_gemv_split": ([_I], _I),
+    "mlq_set_gemm_split": ([_I], _I),
 }
 
 _LIB = None
@@ -304,6 +305,13 @@ def linear_aos(qtype: str, aos_dev, n: int, k: int, x, workspace=None,
 def set_gemv_split(split: int = 0) -> None:
     """Override the GEMV K split (waves per tile; 0 = automatic)."""
     _check(lib().mlq_set_gemv_split(split), "mlq_set_gemv_split")
+
+
+def set_gemm_split(split: int = 0) -> None:
+    """Override the prefill GEMM split-K (workgroups per output tile, each a
+    K range; 0 = planner). Workspaces sized before the change may be too
+    small afterwards: `linear` with workspace="auto" re-queries the size."""
+    _check(lib().mlq_set_gemm_split(split), "mlq_set_gemm_split")
 
 
 def add_bias(y, bias, stream=None):

@@ -206,7 +206,9 @@ int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes) {
   if (rc != MLQ_OK) return rc;
   if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
-  *bytes = uses_gemv(w, m) ? 0 : gemm_workspace_bytes(m, w->k);
+  *bytes = uses_gemv(w, m)           ? 0
+           : m <= kSkinnyMaxRows ? f16_copy_bytes(m, w->k)
+                                 : gemm_workspace_bytes(m, w->n, w->k);
   return MLQ_OK;
 }
 
@@ -219,7 +221,8 @@ int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
   if (m <= 0) return MLQ_ERR_SHAPE;
   const hipStream_t s = (hipStream_t)stream;
   if (uses_gemv(w, m)) return hip_status(launch_gemv(*w, x, y, m, s));
-  const size_t need = gemm_workspace_bytes(m, w->k);
+  const size_t need = m <= kSkinnyMaxRows ? f16_copy_bytes(m, w->k)
+                                           : gemm_workspace_bytes(m, w->n, w->k);
   if (workspace == nullptr || workspace_bytes < need)
     return MLQ_ERR_BUFFER_TOO_SMALL;
   if (((uintptr_t)workspace & 255u) != 0) return MLQ_ERR_INVALID_ARG;
@@ -249,6 +252,12 @@ int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,
   rc = hip_status(launch_repack(type, aos_dev, n, k, w, s));
   if (rc != MLQ_OK) return rc;
   return mlq_linear(&w, x, y, m, stream);
+}
+
+int mlq_set_gemm_split(int split) {
+  if (split < 0 || split > 64) return MLQ_ERR_INVALID_ARG;
+  set_gemm_split(split);
+  return MLQ_OK;
 }
 
 int mlq_set_gemv_split(int split) {

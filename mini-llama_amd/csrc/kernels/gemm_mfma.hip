@@ -33,6 +33,8 @@
 // m (an int8 MFMA variant would need a per-(m, n, block) fp32 fixup).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "../mlq_layout.h"
 #include "device_common.h"
 #include "launch.h"
@@ -57,9 +59,11 @@ struct GemmArgs {
   const float* x;      // fp32 activations [m][k] (XF32 modes)
   const _Float16* xh;  // fp16 activations [m][kp] (XF16 mode, workspace)
   float* y;
+  float* part;         // split-K partial outputs [splits][m][n] (splits > 1)
   int m, n, k, g, nt;
   int kp;              // row stride of xh: k rounded up to whole stages
-  int mtiles, ntiles;  // workgroup grid
+  int mtiles, ntiles;  // output tiles
+  int splits;          // K ranges per output tile (workgroups per tile)
 };
 
 // Activation source: fp32 rows loaded as float4 (k % 4 == 0), fp32 loaded
@@ -252,9 +256,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs a) {
   const int b = blockIdx.x;
   const int full = nwg / kXcds * kXcds;
   const int id = b < full ? (b % kXcds) * (full / kXcds) + b / kXcds : b;
-  const int mt = id % a.mtiles, ntile = id / a.mtiles;
+  // m fastest, then the K range, then the weight column block: the
+  // workgroups that share a weight block's K range are neighbours
+  const int mt = id % a.mtiles, rest = id / a.mtiles;
+  const int sp = rest % a.splits, ntile = rest / a.splits;
   const int m0 = mt * kBM;
   const int tile0 = ntile * kTiles;  // first W row tile
+  // this workgroup's 128-k groups [g0, g1): 2 stages each
+  const int g0 = sp * a.g / a.splits, g1 = (sp + 1) * a.g / a.splits;
+  const int sbase = 2 * g0;
 
   // buffer ranges: rows past m / tiles past nt read as zero
   const int rows = min(kBM, a.m - m0);
@@ -276,8 +286,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int stages = a.g * 2;  // even, >= 2
+  const int stages = 2 * (g1 - g0);  // even, >= 2
   const int last = stages - 1;
+  // stage indices below are relative to the workgroup's K range
+  auto lx = [&](XStage& st, int rel) { load_x<XM>(a, st, rx, sbase + rel, tid); };
+  auto lw = [&](WStage<QT>& st, int rel) {
+    load_w<QT>(a, st, rq, rd, rm, sbase + rel, lane, wn);
+  };
+  auto sx = [&](XStage& st, int slab, int rel) {
+    store_x<XM>(a, st, as_buf[slab], sbase + rel, tid);
+  };
   // fragment rows of this lane: MFMA operand row/col = lane % 32, k octet
   // = lane / 32
   const int fr = lane & 31, fk = 8 * (lane >> 5);
@@ -292,13 +310,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs a) {
   // W(0), W(1) in slots 0 and 1
   XStage xs[2];
   WStage<QT> ws[3];
-  load_x<XM>(a, xs[0], rx, 0, tid);
-  load_w<QT>(a, ws[0], rq, rd, rm, 0, lane, wn);
-  load_x<XM>(a, xs[1], rx, 1, tid);
-  load_w<QT>(a, ws[1], rq, rd, rm, 1, lane, wn);
-  store_x<XM>(a, xs[0], as_buf[0], 0, tid);
-  store_x<XM>(a, xs[1], as_buf[1], 1, tid);
-  load_x<XM>(a, xs[0], rx, min(2, last), tid);
+  lx(xs[0], 0);
+  lw(ws[0], 0);
+  lx(xs[1], 1);
+  lw(ws[1], 1);
+  sx(xs[0], 0, 0);
+  sx(xs[1], 1, 1);
+  lx(xs[0], min(2, last));
   __syncthreads();
 
   h8_t af[4], bf[2];
@@ -317,15 +335,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs a) {
     constexpr int BC = S % 3, BN = (S + 1) % 3, BA = (S + 2) % 3;
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      if (ks == 0) load_x<XM>(a, xs[XA], rx, min(s + 3, last), tid);
-      if (ks == 1) load_w<QT>(a, ws[WA], rq, rd, rm, min(s + 2, last), lane, wn);
+      if (ks == 0) lx(xs[XA], min(s + 3, last));
+      if (ks == 1) lw(ws[WA], min(s + 2, last));
       h8_t an[4], bn[2];
       if (ks < kBK / 16 - 1) {
         read_a(an, BC, ks + 1);
 #pragma unroll
         for (int j = 0; j < 2; ++j) bn[j] = decode_w<QT>(ws[WC], j, ks + 1);
       } else {
-        if (s + 2 < stages) store_x<XM>(a, xs[XC], as_buf[BA], s + 2, tid);
+        if (s + 2 < stages) sx(xs[XC], BA, s + 2);
         read_a(an, BN, 0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) bn[j] = decode_w<QT>(ws[WN], j, 0);
@@ -368,7 +386,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs a) {
   if (s + 4 <= stages) { step(s + 2, Slot<2>{}); step(s + 3, Slot<3>{}); }
 
   // epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each
-  // 32x32 block
+  // 32x32 block; with several K ranges each writes its own partial slice
+  float* out = a.splits > 1 ? a.part + (size_t)sp * a.m * a.n : a.y;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -378,9 +397,32 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int mrow = m0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (mrow < a.m) a.y[(size_t)mrow * a.n + ncol] = acc[i][j][r];
+        if (mrow < a.m) out[(size_t)mrow * a.n + ncol] = acc[i][j][r];
       }
     }
+  }
+}
+
+// y = sum of the split-K partial slices, in slice order (deterministic).
+// VEC: count % 4 == 0, four outputs per thread.
+template <bool VEC>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* part,
+                                                           float* y,
+                                                           size_t count,
+                                                           int splits) {
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * (VEC ? 4 : 1);
+  if (i >= count) return;
+  if (VEC) {
+    float4 s = *(const float4*)(part + i);
+    for (int p = 1; p < splits; ++p) {
+      const float4 v = *(const float4*)(part + (size_t)p * count + i);
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+    *(float4*)(y + i) = s;
+  } else {
+    float s = part[i];
+    for (int p = 1; p < splits; ++p) s += part[(size_t)p * count + i];
+    y[i] = s;
   }
 }
 
@@ -414,14 +456,42 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const float* x,
 
 template <int QT>
 hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
-  const unsigned grid = (unsigned)(a.mtiles * a.ntiles);
+  const unsigned grid = (unsigned)(a.mtiles * a.ntiles * a.splits);
   switch (xm) {
     case kXF32Vec: gemm_kernel<QT, kXF32Vec><<<grid, kThreads, 0, stream>>>(a); break;
     case kXF32Scalar: gemm_kernel<QT, kXF32Scalar><<<grid, kThreads, 0, stream>>>(a); break;
     default: gemm_kernel<QT, kXF16><<<grid, kThreads, 0, stream>>>(a); break;
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  const size_t count = (size_t)a.m * a.n;
+  if (count % 4 == 0) {
+    const size_t threads = count / 4;
+    split_reduce_kernel<true><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
+        a.part, a.y, count, a.splits);
+  } else {
+    split_reduce_kernel<false><<<(unsigned)((count + 255) / 256), 256, 0, stream>>>(
+        a.part, a.y, count, a.splits);
+  }
   return hipGetLastError();
 }
+
+// Compute units of the current device (256 on MI355X), read once.
+int device_cus() {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      return 256;
+    return n;
+  }();
+  return cus;
+}
+
+int g_split_override = 0;  // mlq_set_gemm_split; 0 = planner
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 }  // namespace
 
@@ -429,8 +499,41 @@ hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
 // every stage (GEMM) and group (skinny GEMM) of a row stays inside it.
 int f16_row_stride(int k) { return (k + kGroupK - 1) / kGroupK * kGroupK; }
 
-size_t gemm_workspace_bytes(int m, int k) {
-  return (size_t)m * f16_row_stride(k) * 2;
+size_t f16_copy_bytes(int m, int k) { return (size_t)m * f16_row_stride(k) * 2; }
+
+void set_gemm_split(int split) { g_split_override = split; }
+
+// K ranges per output tile. One workgroup runs per CU (one wave per SIMD)
+// and its K loop is serial, so a shape with few tiles (small m, or small n)
+// leaves CUs idle for the whole K loop. Splitting K multiplies the
+// workgroups; each split then writes an fp32 partial slice that a reduce
+// pass sums in order. Cost model (us), fitted to measurements on MI355X:
+// a 64-k stage takes 0.66 us for a lone workgroup and 0.0018 us more per
+// workgroup running beside it (shared L2 / HBM), ~2 us of prologue and
+// epilogue per round of workgroups, partial slices written and read at
+// ~4 TB/s, ~2 us for the reduce launch.
+int gemm_splits(int m, int n, int k) {
+  const int g = (k + kGroupK - 1) / kGroupK;
+  if (g_split_override > 0) return std::min(g_split_override, g);
+  const int tiles = (m + kBM - 1) / kBM * ((n + kBN - 1) / kBN);
+  const int cus = device_cus();
+  int best = 1;
+  double best_t = 0.0;
+  for (int sp = 1; sp <= 16 && sp <= g; ++sp) {
+    const int wgs = tiles * sp;
+    const int rounds = (wgs + cus - 1) / cus;
+    const int stages = 2 * ((g + sp - 1) / sp);
+    const double stage_us = 0.66 + 0.0018 * std::min(wgs, cus);
+    double t = rounds * (stages * stage_us + 2.0);
+    if (sp > 1) t += (2.0 * sp + 1.0) * m * (double)n * 4.0 / 4.0e6 + 2.0;
+    if (sp == 1 || t < best_t) { best = sp; best_t = t; }
+  }
+  return best;
+}
+
+size_t gemm_workspace_bytes(int m, int n, int k) {
+  const int sp = gemm_splits(m, n, k);
+  return align256(f16_copy_bytes(m, k)) + (sp > 1 ? (size_t)sp * m * n * 4 : 0);
 }
 
 hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,
@@ -465,16 +568,24 @@ hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
   a.kp = f16_row_stride(w.k);
   a.mtiles = (m + kBM - 1) / kBM;
   a.ntiles = (geo.nt + kTiles - 1) / kTiles;
+  a.splits = 1;
+  a.part = nullptr;
   // every activation row offset of a workgroup must fit a 32-bit buffer
   // offset
   if ((size_t)kBM * (size_t)w.k * 4 >= (1ull << 31)) return hipErrorInvalidValue;
   int xm = (w.k & 3) == 0 ? kXF32Vec : kXF32Scalar;
-  if (ws != nullptr && ws_bytes >= gemm_workspace_bytes(m, w.k)) {
+  if (ws != nullptr && ws_bytes >= f16_copy_bytes(m, w.k)) {
     // one pass over x: fp16 copy, row stride kp, zero tail
     a.xh = (_Float16*)ws;
     const hipError_t e = launch_x_to_f16(x, (_Float16*)ws, m, w.k, stream);
     if (e != hipSuccess) return e;
     xm = kXF16;
+    // split K when the workspace also holds the partial slices
+    const int sp = gemm_splits(m, w.n, w.k);
+    if (sp > 1 && ws_bytes >= gemm_workspace_bytes(m, w.n, w.k)) {
+      a.splits = sp;
+      a.part = (float*)((uint8_t*)ws + align256(f16_copy_bytes(m, w.k)));
+    }
   }
   switch (w.type) {
     case MLQ_Q8_0: return launch_typed<MLQ_Q8_0>(a, xm, stream);

@@ -27,12 +27,19 @@ int gemv_max_k(int type, int m);
 void set_gemv_split(int split);
 
 // gemm_mfma.hip: any m >= 1. The _ws form converts x to fp16 into `ws`
-// first when ws_bytes >= gemm_workspace_bytes(m, k) (else reads fp32 x).
+// first when ws_bytes >= f16_copy_bytes(m, k) (else reads fp32 x), and
+// splits K over gemm_splits(m, n, k) workgroups per output tile when
+// ws_bytes >= gemm_workspace_bytes(m, n, k) (fp32 partial slices after the
+// fp16 copy, summed in order by a second kernel).
 hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream);
 hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
                           void* ws, size_t ws_bytes, hipStream_t stream);
-size_t gemm_workspace_bytes(int m, int k);
+size_t f16_copy_bytes(int m, int k);
+int gemm_splits(int m, int n, int k);
+size_t gemm_workspace_bytes(int m, int n, int k);
+// Split-K override (0 = planner); validated by the caller.
+void set_gemm_split(int split);
 // fp16 copy of x [m][k] into xh [m][f16_row_stride(k)] (zero past k).
 int f16_row_stride(int k);
 hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,

@@ -231,7 +231,17 @@ def test_gemm_workspace_path_matches_direct(pkg, cuda, qtype, m, n, k):
     got_ws = pkg.linear(tw, xd, workspace=ws).cpu().numpy()
     got_direct = pkg.linear(tw, xd, path=pkg.PATH_MFMA).cpu().numpy()
     if m > 64:
-        assert np.array_equal(got_ws, got_direct)
+        # the planner may split K (another fp32 summation order); one K
+        # range per tile must reproduce the direct GEMM bit for bit
+        x = make_x(m, k, seed=k)
+        atol = 1e-3 * np.linalg.norm(x, axis=1, keepdims=True) * np.sqrt(k / 4096)
+        assert np.all(np.abs(got_ws - got_direct) <= 1e-3 * atol)
+        pkg.set_gemm_split(1)
+        try:
+            got_one = pkg.linear(tw, xd, workspace=ws).cpu().numpy()
+        finally:
+            pkg.set_gemm_split(0)
+        assert np.array_equal(got_one, got_direct)
     else:
         # 9..64 rows take the skinny GEMM: same fp16 operands, another fp32
         # summation order
@@ -246,6 +256,43 @@ def test_gemm_workspace_path_matches_direct(pkg, cuda, qtype, m, n, k):
         pkg.linear(tw, xd, workspace=big[16:])  # large enough, misaligned
     assert e.value.status == -1
     assert pkg.workspace_bytes(tw, 1) == 0  # decode GEMV needs none
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("split", [1, 2, 3, 5, 8])
+def test_gemm_every_split(pkg, oracle, cuda, qtype, split):
+    """Split-K prefill GEMM: every K range count (uneven ranges when the
+    groups do not divide, ranges of one group, splits capped at the group
+    count), partial slices summed in order; checked against the oracle and
+    against the unsplit kernel."""
+    torch = _torch()
+    _print_case(test="gemm_split", qtype=qtype, split=split)
+    try:
+        for m, n, k in [(65, 48, 1000), (130, 300, 2100), (200, 17, 640),
+                        (129, 40, 4096), (96, 33, 300)]:
+            blocks = make_blocks(qtype, n, k, seed=n + k + m)
+            x = make_x(m, k, seed=k + 7)
+            tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+            xd = _dev(x, cuda)
+            pkg.set_gemm_split(1)
+            ws = torch.empty(pkg.workspace_bytes(tw, m), dtype=torch.uint8, device=cuda)
+            one = pkg.linear(tw, xd, workspace=ws).cpu().numpy()
+            pkg.set_gemm_split(split)
+            need = pkg.workspace_bytes(tw, m)
+            groups = -(-k // 128)
+            if min(split, groups) > 1:
+                assert need >= m * n * 4 * min(split, groups)
+            ws = torch.empty(need, dtype=torch.uint8, device=cuda)
+            got = pkg.linear(tw, xd, workspace=ws).cpu().numpy()
+            ref = oracle.linear(x, blocks, (n, k), qtype, threads=8)
+            # fp16 operands (the prefill GEMM's numerics): the stated bar
+            assert tolerance_ok(got, ref, x, k).all(), (m, n, k, error_report(got, ref, x, k))
+            atol = 1e-3 * np.linalg.norm(x, axis=1, keepdims=True) * np.sqrt(k / 4096)
+            assert np.all(np.abs(got - one) <= 1e-3 * atol), (m, n, k)
+            again = pkg.linear(tw, xd, workspace=ws).cpu().numpy()
+            assert np.array_equal(got, again)  # fixed summation order
+    finally:
+        pkg.set_gemm_split(0)
 
 
 @pytest.mark.parametrize("m", [1, 3, 16])
