@@ -207,7 +207,7 @@ int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes) {
   if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
   *bytes = uses_gemv(w, m)           ? 0
-           : m <= kSkinnyMaxRows ? f16_copy_bytes(m, w->k)
+           : m <= kSkinnyMaxRows ? skinny_x_bytes(m, w->k)
                                  : gemm_workspace_bytes(m, w->n, w->k);
   return MLQ_OK;
 }
@@ -221,17 +221,17 @@ int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
   if (m <= 0) return MLQ_ERR_SHAPE;
   const hipStream_t s = (hipStream_t)stream;
   if (uses_gemv(w, m)) return hip_status(launch_gemv(*w, x, y, m, s));
-  const size_t need = m <= kSkinnyMaxRows ? f16_copy_bytes(m, w->k)
+  const size_t need = m <= kSkinnyMaxRows ? skinny_x_bytes(m, w->k)
                                            : gemm_workspace_bytes(m, w->n, w->k);
   if (workspace == nullptr || workspace_bytes < need)
     return MLQ_ERR_BUFFER_TOO_SMALL;
   if (((uintptr_t)workspace & 255u) != 0) return MLQ_ERR_INVALID_ARG;
   if (m <= kSkinnyMaxRows) {
-    // batched decode: fp16 copy of x, then the skinny GEMM
-    _Float16* xh = (_Float16*)workspace;
-    rc = hip_status(launch_x_to_f16(x, xh, m, w->k, s));
+    // batched decode: fragment-ordered fp16 copy of x, then the skinny GEMM
+    _Float16* xf = (_Float16*)workspace;
+    rc = hip_status(launch_x_to_frag(x, xf, m, w->k, s));
     if (rc != MLQ_OK) return rc;
-    return hip_status(launch_skinny(*w, xh, f16_row_stride(w->k), y, m, s));
+    return hip_status(launch_skinny(*w, xf, y, m, s));
   }
   return hip_status(launch_gemm_ws(*w, x, y, m, workspace, workspace_bytes, s));
 }

@@ -45,9 +45,13 @@ int f16_row_stride(int k);
 hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,
                            hipStream_t stream);
 
-// skinny.hip: 9..64 rows of x from its fp16 copy (row stride kp).
+// skinny.hip: 9..64 rows of x from its fragment-ordered fp16 copy
+// (skinny_x_bytes(m, k) bytes, made by launch_x_to_frag).
 constexpr int kSkinnyMaxRows = 64;
-hipError_t launch_skinny(const mlq_weight& w, const _Float16* xh, int kp,
-                         float* y, int m, hipStream_t stream);
+size_t skinny_x_bytes(int m, int k);
+hipError_t launch_x_to_frag(const float* x, _Float16* xf, int m, int k,
+                            hipStream_t stream);
+hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int m,
+                         hipStream_t stream);
 
 }  // namespace mlq

@@ -4,19 +4,25 @@
 // Between the decode GEMV (m <= 8) and the prefill GEMM (128-row tiles)
 // neither fits: a 128-row activation tile wastes most of its MFMA rows and,
 // with N = 4096, gives only 32 workgroups. This kernel keeps the GEMV's
-// grid (one workgroup per 16-row weight tile, its waves splitting K, so the
+// grid (workgroups over 16-row weight tiles, their waves splitting K, so the
 // weights stream from HBM once with 256+ workgroups in flight) and runs the
 // rows of x through v_mfma_f32_16x16x32_f16 in blocks of 16:
-//  - x comes from the fp16 copy that mlq_linear_ws makes first (rows of kp
-//    halves, zero past k). An MFMA A fragment is 16 contiguous bytes of one
-//    row, so waves load fragments straight from that copy (L2-resident)
-//    instead of staging x in LDS.
+//  - x comes from an fp16 copy that mlq_linear_ws makes first, written in
+//    MFMA fragment order (rows padded to 16; per 128-k group, row block and
+//    32-k block one run of 64 lanes x 16 bytes), so every x fragment load
+//    of a wave is 1 KiB contiguous (L2-resident). x is re-read by every
+//    workgroup: its load volume, not the weight stream, bounds the kernel
+//    once m >= 32.
+//  - A workgroup covers T = 1, 2 or 4 weight tiles and reuses each x
+//    fragment for all of them (T chosen so that at least 256 workgroups
+//    remain), dividing the x traffic by T.
 //  - Weights: one 1 KiB (q4) / 2 KiB (q8) line per (tile, 128-k group) as in
 //    the GEMV; codes are decoded exactly and scaled by d in fp16 (one
 //    rounding, the prefill GEMM's numerics), so the MFMA accumulates across
 //    blocks with no per-block fixup.
-//  - Group g+1's weight line and x fragments are requested before group g's
-//    MFMAs run. K slices combine through LDS in slice order.
+//  - Group g+1's weight lines and x fragments are requested before group
+//    g's MFMAs run. K slices combine through LDS in slice order, one tile
+//    at a time.
 #include <hip/hip_runtime.h>
 
 #include "../mlq_layout.h"
@@ -33,41 +39,42 @@ struct SkinnyArgs {
   const uint8_t* qs;
   const uint8_t* d;
   const uint8_t* mn;
-  const _Float16* xh;  // [m][kp] fp16, zero past k
+  const _Float16* xf;  // fragment-ordered fp16 copy of x (skinny_x_bytes)
   float* y;
-  int m, n, g, kp;
-  int gw;  // groups per wave
+  int m, n, g, nt;
 };
 
-template <int QT, int MB>
+// One 128-k group of T weight tiles and the x fragments of all row blocks.
+template <int QT, int MB, int T>
 struct Group {
-  uint4 q, q2;   // weight line chunk(s)
-  uint2 d, mm;   // four fp16 scales / mins
-  uint4 a[MB][4];  // x fragments: m block, weight block
+  uint4 q[T], q2[T];  // weight line chunk(s) per tile
+  uint2 d[T], mm[T];  // four fp16 scales / mins per tile
+  uint4 a[MB][4];     // x fragments: m block, weight block
 };
 
-template <int QT, int MB>
-__device__ __forceinline__ void load_group(const SkinnyArgs& a, Group<QT, MB>& gr,
-                                           rsrc_t rq, rsrc_t rd, rsrc_t rm,
+template <int QT, int MB, int T>
+__device__ __forceinline__ void load_group(Group<QT, MB, T>& gr, const rsrc_t (&rq)[T],
+                                           const rsrc_t (&rd)[T], const rsrc_t (&rm)[T],
                                            rsrc_t rx, int j, int lane) {
   const uint32_t unit = (uint32_t)j;  // relative to the wave's first unit
-  if (QT == MLQ_Q8_0) {
-    gr.q = buf_load16_stream(rq, ((unit * 2) * 64 + lane) * 16, 0);
-    gr.q2 = buf_load16_stream(rq, ((unit * 2 + 1) * 64 + lane) * 16, 0);
-  } else {
-    gr.q = buf_load16_stream(rq, (unit * 64 + lane) * 16, 0);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    if (QT == MLQ_Q8_0) {
+      gr.q[t] = buf_load16_stream(rq[t], ((unit * 2) * 64 + lane) * 16, 0);
+      gr.q2[t] = buf_load16_stream(rq[t], ((unit * 2 + 1) * 64 + lane) * 16, 0);
+    } else {
+      gr.q[t] = buf_load16_stream(rq[t], (unit * 64 + lane) * 16, 0);
+    }
+    const uint32_t soff = (unit * kTileRows + (lane & 15)) * 8;
+    gr.d[t] = buf_load8(rd[t], soff, 0);
+    if (QT == MLQ_Q4_1) gr.mm[t] = buf_load8(rm[t], soff, 0);
   }
-  const uint32_t soff = (unit * kTileRows + (lane & 15)) * 8;
-  gr.d = buf_load8(rd, soff, 0);
-  if (QT == MLQ_Q4_1) gr.mm = buf_load8(rm, soff, 0);
-  // A fragment of block b, m block mb: row 16mb + lane%16, k 32b + 8(lane/16)
-  const int r = lane & 15, kq = lane >> 4;
+  // A fragment of block b, row block mb: 64 lanes x 16 bytes, contiguous
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      gr.a[mb][b] = buf_load16(
-          rx, (uint32_t)(((16 * mb + r) * a.kp + j * kGroupK + 32 * b + 8 * kq) * 2), 0);
+      gr.a[mb][b] = buf_load16(rx, (uint32_t)((((j * MB + mb) * 4 + b) * 64 + lane) * 16), 0);
 }
 
 __device__ __forceinline__ h2_t splat(uint2 s, int b) {
@@ -76,14 +83,14 @@ __device__ __forceinline__ h2_t splat(uint2 s, int b) {
   return (h2_t){v, v};
 }
 
-// B fragment of block b: 8 codes of quarter lane/16 of row lane%16, decoded
-// exactly and scaled in fp16.
-template <int QT, int MB>
-__device__ __forceinline__ h8_t decode(const Group<QT, MB>& gr, int b) {
-  const h2_t d2 = splat(gr.d, b);
+// B fragment of block b of tile t: 8 codes of quarter lane/16 of row
+// lane%16, decoded exactly and scaled in fp16.
+template <int QT, int MB, int T>
+__device__ __forceinline__ h8_t decode(const Group<QT, MB, T>& gr, int t, int b) {
+  const h2_t d2 = splat(gr.d[t], b);
   uint4 o;
   if (QT == MLQ_Q8_0) {
-    const uint4 q = b < 2 ? gr.q : gr.q2;
+    const uint4 q = b < 2 ? gr.q[t] : gr.q2[t];
     const uint32_t w0 = (b & 1) ? q.z : q.x, w1 = (b & 1) ? q.w : q.y;
     const h2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
     uint32_t p0, p1, p2, p3;
@@ -94,7 +101,8 @@ __device__ __forceinline__ h8_t decode(const Group<QT, MB>& gr, int b) {
     o.z = as_u32((as_h2(p2) - bias) * d2);
     o.w = as_u32((as_h2(p3) - bias) * d2);
   } else {
-    const uint32_t w = b == 0 ? gr.q.x : b == 1 ? gr.q.y : b == 2 ? gr.q.z : gr.q.w;
+    const uint4 qq = gr.q[t];
+    const uint32_t w = b == 0 ? qq.x : b == 1 ? qq.y : b == 2 ? qq.z : qq.w;
     const float lo = QT == MLQ_Q4_0 ? 1032.0f : 1024.0f;
     const float hi = QT == MLQ_Q4_0 ? 72.0f : 64.0f;
     const h2_t blo = {(_Float16)lo, (_Float16)lo};
@@ -106,7 +114,7 @@ __device__ __forceinline__ h8_t decode(const Group<QT, MB>& gr, int b) {
       o.z = as_u32((as_h2(p.p2) - blo) * d2);
       o.w = as_u32((as_h2(p.p3) - bhi) * d2);
     } else {
-      const h2_t m2 = splat(gr.mm, b);
+      const h2_t m2 = splat(gr.mm[t], b);
       o.x = as_u32(__builtin_elementwise_fma(as_h2(p.p0) - blo, d2, m2));
       o.y = as_u32(__builtin_elementwise_fma(as_h2(p.p1) - bhi, d2, m2));
       o.z = as_u32(__builtin_elementwise_fma(as_h2(p.p2) - blo, d2, m2));
@@ -116,40 +124,53 @@ __device__ __forceinline__ h8_t decode(const Group<QT, MB>& gr, int b) {
   return __builtin_bit_cast(h8_t, o);
 }
 
-template <int QT, int MB>
+template <int QT, int MB, int T>
 __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyArgs a) {
   __shared__ float part[kWaves * 64 * 16];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tile = blockIdx.x;
-  const int g0 = wave * a.gw;
-  const int ng = max(0, min(a.gw, a.g - g0));
+  const int t0 = blockIdx.x * T;
+  const int gw = (a.g + kWaves - 1) / kWaves;
+  const int g0 = wave * gw;
+  const int ng = max(0, min(gw, a.g - g0));
 
   constexpr uint32_t QB = QT == MLQ_Q8_0 ? 2048u : 1024u;
-  const size_t unit0 = (size_t)tile * a.g + g0;
-  const rsrc_t rq = make_rsrc(a.qs + unit0 * QB, (uint32_t)ng * QB);
-  const rsrc_t rd = make_rsrc(a.d + unit0 * 128, (uint32_t)ng * 128u);
-  const rsrc_t rm = QT == MLQ_Q4_1 ? make_rsrc(a.mn + unit0 * 128, (uint32_t)ng * 128u) : rd;
-  // x fragments of this wave's k range; rows past m read as zero
-  const rsrc_t rx = make_rsrc(a.xh + (size_t)g0 * kGroupK,
-                              (uint32_t)(((size_t)(a.m - 1) * a.kp + (size_t)ng * kGroupK) * 2));
-
-  f4_t acc[MB];
+  rsrc_t rq[T], rd[T], rm[T];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = (f4_t){0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < T; ++t) {
+    // tiles past nt read as zero
+    const int tile = min(t0 + t, a.nt - 1);
+    const uint32_t units = t0 + t < a.nt ? (uint32_t)ng : 0u;
+    const size_t unit0 = (size_t)tile * a.g + g0;
+    rq[t] = make_rsrc(a.qs + unit0 * QB, units * QB);
+    rd[t] = make_rsrc(a.d + unit0 * 128, units * 128u);
+    rm[t] = QT == MLQ_Q4_1 ? make_rsrc(a.mn + unit0 * 128, units * 128u) : rd[t];
+  }
+  // this wave's groups of the fragment-ordered x (padded rows are zero)
+  const rsrc_t rx = make_rsrc(a.xf + (size_t)g0 * MB * 16 * kGroupK,
+                              (uint32_t)((size_t)ng * MB * 16 * kGroupK * 2));
 
-  Group<QT, MB> gr[2];
-  if (ng > 0) load_group<QT, MB>(a, gr[0], rq, rd, rm, rx, 0, lane);
-  auto run = [&](Group<QT, MB>& cur, Group<QT, MB>& nxt, int j) {
-    if (j + 1 < ng) load_group<QT, MB>(a, nxt, rq, rd, rm, rx, j + 1, lane);
+  f4_t acc[T][MB];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[t][mb] = (f4_t){0.f, 0.f, 0.f, 0.f};
+
+  Group<QT, MB, T> gr[2];
+  if (ng > 0) load_group<QT, MB, T>(gr[0], rq, rd, rm, rx, 0, lane);
+  auto run = [&](Group<QT, MB, T>& cur, Group<QT, MB, T>& nxt, int j) {
+    if (j + 1 < ng) load_group<QT, MB, T>(nxt, rq, rd, rm, rx, j + 1, lane);
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const h8_t bf = decode<QT, MB>(cur, b);
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(h8_t, cur.a[mb][b]), bf, acc[mb], 0, 0, 0);
+      for (int t = 0; t < T; ++t) {
+        const h8_t bf = decode<QT, MB, T>(cur, t, b);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          acc[t][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(h8_t, cur.a[mb][b]), bf, acc[t][mb], 0, 0, 0);
+      }
     }
   };
   int j = 0;
@@ -160,59 +181,127 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyArgs a) {
   if (j < ng) run(gr[0], gr[1], j);
 
   // lane holds D[4*(lane/16) + i][lane%16]: activation row 16mb + 4(lane/16)
-  // + i, weight row lane%16. K slices combine in slice order.
+  // + i, weight row lane%16 of tile t. K slices combine in slice order, one
+  // tile at a time.
   const int col = lane & 15, rq4 = 4 * (lane >> 4);
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int t = 0; t < T; ++t) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      part[(wave * 64 + 16 * mb + rq4 + i) * 16 + col] = acc[mb][i];
-  __syncthreads();
-  for (int o = tid; o < a.m * 16; o += kThreads) {
-    const int r = o / 16, c = o % 16;
-    float s = 0.0f;
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) s += part[(w * 64 + r) * 16 + c];
-    const int row = tile * kTileRows + c;
-    if (row < a.n) a.y[(size_t)r * a.n + row] = s;
+      for (int i = 0; i < 4; ++i)
+        part[(wave * 64 + 16 * mb + rq4 + i) * 16 + col] = acc[t][mb][i];
+    __syncthreads();
+    for (int o = tid; o < a.m * 16; o += kThreads) {
+      const int r = o / 16, c = o % 16;
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) s += part[(w * 64 + r) * 16 + c];
+      const int row = (t0 + t) * kTileRows + c;
+      if (row < a.n) a.y[(size_t)r * a.n + row] = s;
+    }
+    if (t + 1 < T) __syncthreads();
   }
 }
 
-template <int QT>
-hipError_t launch_typed(const SkinnyArgs& a, int nt, hipStream_t stream) {
+// x fp32 [m][k] -> the fragment-ordered fp16 copy: element (r, c) of row
+// block mb = r/16, 128-k group j = c/128, 32-k block b = c%128/32 sits at
+// lane r%16 + 16*(c%32/8), position c%8 of run ((j*mbt + mb)*4 + b);
+// rows >= m and columns >= k are zero. One thread per 16-byte chunk.
+__global__ __launch_bounds__(256) void x_to_frag_kernel(const float* x, _Float16* xf,
+                                                        int m, int k, int kp, int mbt) {
+  const int per_row = kp / 8;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)mbt * 16 * per_row) return;
+  const int r = (int)(idx / per_row), c0 = (int)(idx % per_row) * 8;
+  float v[8];
+  const float* xr = x + (size_t)r * k;
+  if (r < m && (k & 3) == 0 && c0 + 8 <= k) {
+    const float4 lo = *(const float4*)(xr + c0);
+    const float4 hi = *(const float4*)(xr + c0 + 4);
+    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (r < m && c0 + e < k) ? xr[c0 + e] : 0.0f;
+  }
+  uint4 o;
+  o.x = pack_h2(v[0], v[1]);
+  o.y = pack_h2(v[2], v[3]);
+  o.z = pack_h2(v[4], v[5]);
+  o.w = pack_h2(v[6], v[7]);
+  const int j = c0 / kGroupK, b = (c0 % kGroupK) / 32, kq = (c0 % 32) / 8;
+  const int mb = r / 16, lane = r % 16 + 16 * kq;
+  *(uint4*)(xf + ((((size_t)j * mbt + mb) * 4 + b) * 64 + lane) * 8) = o;
+}
+
+// Weight tiles per workgroup: reuse each x fragment for up to four tiles
+// while at least 256 workgroups remain (measured: T = 4 at N = 18944, 2 at
+// N = 11008, 1 at N = 4096).
+int tiles_per_group(int nt) {
+  if (nt / 4 >= 256) return 4;
+  if (nt / 2 >= 256) return 2;
+  return 1;
+}
+
+template <int QT, int T>
+hipError_t launch_t(const SkinnyArgs& a, hipStream_t stream) {
   const int mb = (a.m + 15) / 16;
+  const unsigned grid = (unsigned)((a.nt + T - 1) / T);
   switch (mb) {
-    case 1: skinny_kernel<QT, 1><<<nt, kThreads, 0, stream>>>(a); break;
-    case 2: skinny_kernel<QT, 2><<<nt, kThreads, 0, stream>>>(a); break;
-    case 3: skinny_kernel<QT, 3><<<nt, kThreads, 0, stream>>>(a); break;
-    default: skinny_kernel<QT, 4><<<nt, kThreads, 0, stream>>>(a); break;
+    case 1: skinny_kernel<QT, 1, T><<<grid, kThreads, 0, stream>>>(a); break;
+    case 2: skinny_kernel<QT, 2, T><<<grid, kThreads, 0, stream>>>(a); break;
+    case 3: skinny_kernel<QT, 3, T><<<grid, kThreads, 0, stream>>>(a); break;
+    default: skinny_kernel<QT, 4, T><<<grid, kThreads, 0, stream>>>(a); break;
   }
   return hipGetLastError();
 }
 
+template <int QT>
+hipError_t launch_typed(const SkinnyArgs& a, hipStream_t stream) {
+  switch (tiles_per_group(a.nt)) {
+    case 1: return launch_t<QT, 1>(a, stream);
+    case 2: return launch_t<QT, 2>(a, stream);
+    default: return launch_t<QT, 4>(a, stream);
+  }
+}
+
 }  // namespace
 
-hipError_t launch_skinny(const mlq_weight& w, const _Float16* xh, int kp,
-                         float* y, int m, hipStream_t stream) {
-  if (m < 1 || m > kSkinnyMaxRows || kp % kGroupK != 0) return hipErrorInvalidValue;
+size_t skinny_x_bytes(int m, int k) {
+  const size_t kp = (size_t)(k + kGroupK - 1) / kGroupK * kGroupK;
+  return (size_t)(m + 15) / 16 * 16 * kp * 2;
+}
+
+hipError_t launch_x_to_frag(const float* x, _Float16* xf, int m, int k,
+                            hipStream_t stream) {
+  const int kp = (k + kGroupK - 1) / kGroupK * kGroupK;
+  const int mbt = (m + 15) / 16;
+  const size_t items = (size_t)mbt * 16 * (kp / 8);
+  x_to_frag_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(x, xf, m, k, kp, mbt);
+  return hipGetLastError();
+}
+
+hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int m,
+                         hipStream_t stream) {
+  if (m < 1 || m > kSkinnyMaxRows) return hipErrorInvalidValue;
+  // 32-bit buffer offsets for the x fragments of a wave
+  if (skinny_x_bytes(m, w.k) >= (1ull << 31)) return hipErrorInvalidValue;
   const Geometry geo = geometry(w.n, w.k);
   SkinnyArgs a;
   a.qs = (const uint8_t*)w.base + w.qs_off;
   a.d = (const uint8_t*)w.base + w.d_off;
   a.mn = w.type == MLQ_Q4_1 ? (const uint8_t*)w.base + w.m_off : nullptr;
-  a.xh = xh;
+  a.xf = xf;
   a.y = y;
   a.m = m;
   a.n = w.n;
   a.g = geo.g;
-  a.kp = kp;
-  a.gw = (geo.g + kWaves - 1) / kWaves;
-  // 32-bit buffer offsets for the x fragments of a wave
-  if ((size_t)m * kp * 2 >= (1ull << 31)) return hipErrorInvalidValue;
+  a.nt = geo.nt;
   switch (w.type) {
-    case MLQ_Q8_0: return launch_typed<MLQ_Q8_0>(a, geo.nt, stream);
-    case MLQ_Q4_0: return launch_typed<MLQ_Q4_0>(a, geo.nt, stream);
-    default: return launch_typed<MLQ_Q4_1>(a, geo.nt, stream);
+    case MLQ_Q8_0: return launch_typed<MLQ_Q8_0>(a, stream);
+    case MLQ_Q4_0: return launch_typed<MLQ_Q4_0>(a, stream);
+    default: return launch_typed<MLQ_Q4_1>(a, stream);
   }
 }
 

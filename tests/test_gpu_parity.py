@@ -150,6 +150,9 @@ SHAPES = [(1, 16, 32), (1, 17, 33), (1, 100, 1000), (1, 300, 4096),
           (5, 33, 4096), (16, 256, 512), (64, 128, 1024), (130, 70, 300),
           # skinny GEMM: rows not a multiple of 16, k not a multiple of 128
           (33, 48, 1001), (50, 17, 4000), (9, 300, 33),
+          # skinny GEMM with 2 and 4 weight tiles per workgroup, the last
+          # workgroup partly past N
+          (16, 8200, 256), (40, 16400, 300),
           (257, 300, 256),
           # one-wave workgroups with m > 4 (fewer threads than m*16 outputs)
           (5, 100, 512), (8, 40, 256), (6, 20, 100)]
@@ -215,7 +218,8 @@ def test_linear_1d_input_and_aos_path(pkg, oracle, cuda, qtype):
 
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("m,n,k", [(9, 40, 200), (130, 70, 300), (64, 256, 4096),
-                                   (300, 100, 1001), (33, 48, 1001), (50, 17, 4000)])
+                                   (300, 100, 1001), (33, 48, 1001), (50, 17, 4000),
+                                   (16, 8200, 256), (61, 16400, 300)])
 def test_gemm_workspace_path_matches_direct(pkg, cuda, qtype, m, n, k):
     """mlq_linear_ws (fp16 copy of x made by a pre-pass) and the direct GEMM
     (x converted inside) round x to fp16 identically, so they must agree bit
