@@ -397,7 +397,7 @@ int split_override() {
 
 struct Plan {
   int split, gw;
-  int depth;  // GW: groups in flight per wave (1..8)
+  int depth;  // GW: groups in flight per wave (1..10)
   bool ring;  // slices longer than max_depth groups: ring of `depth` slots
   int padded; // groups staged per wave (gw, or whole ring passes)
   size_t wave_lds, lds;
@@ -405,11 +405,14 @@ struct Plan {
 
 // Groups in flight per wave without spilling (VGPR budget of a 1024-thread
 // workgroup): every group of the slice when gw <= max_depth, else a ring.
-// q4_1 carries mins and block sums per group, so its budgets are smaller.
+// q4_1 carries mins and block sums per group, so its budgets are smaller;
+// one activation row leaves room for ten (long-K shapes with few tiles,
+// e.g. the 3584 x 18944 down-projection, keep more bytes in flight).
 constexpr int kMaxDepth = 8;
+constexpr int kMaxDepthOneRow = 10;
 int max_depth(int type, int m) {
   if (type == MLQ_Q4_1) return m == 1 ? 6 : 3;
-  return kMaxDepth;
+  return m == 1 ? kMaxDepthOneRow : kMaxDepth;
 }
 // Ring depths that compile without spills, per type and row class.
 int ring_depth_lo(int type, int m) { return type == MLQ_Q4_1 ? (m == 1 ? 3 : 2) : 4; }
@@ -529,7 +532,14 @@ hipError_t launch_depth(const GemvArgs& a, const Plan& p, hipStream_t stream) {
     case 5: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 5, false>(a, p.lds, stream);
     case 6: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 6, false>(a, p.lds, stream);
     case 7: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 7, false>(a, p.lds, stream);
-    default: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 8, false>(a, p.lds, stream);
+    case 8: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 8, false>(a, p.lds, stream);
+    default:
+      // 9 and 10: one activation row, q8_0 / q4_0 only
+      if constexpr (QT != MLQ_Q4_1 && MR == 1) {
+        if (p.depth == 9) return launch_typed<QT, MR, 9, false>(a, p.lds, stream);
+        return launch_typed<QT, MR, 10, false>(a, p.lds, stream);
+      }
+      return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 8, false>(a, p.lds, stream);
   }
 }
 

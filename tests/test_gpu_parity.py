@@ -184,12 +184,13 @@ def test_gemv_every_split(pkg, oracle, cuda, qtype, split):
     """Every GEMV K split on shapes that take each code path: slices of
     1..8 groups all in flight, slices longer than the in-flight budget (the
     refill ring), a shorter last slice (groups % split != 0), k % 4 != 0
-    (element-wise activation loads) and 1, 2, 3 and 8 activation rows."""
+    (element-wise activation loads), slices of 9 and 10 groups in flight
+    (one activation row) and 1, 2, 3 and 8 activation rows."""
     _print_case(test="gemv_split", qtype=qtype, split=split)
     pkg.set_gemv_split(split)
     try:
         for m, n, k in [(1, 48, 4000), (3, 40, 2100), (8, 17, 1500),
-                        (2, 20, 1001), (1, 33, 9000)]:
+                        (2, 20, 1001), (1, 33, 9000), (1, 20, 5000)]:
             blocks = make_blocks(qtype, n, k, seed=n + k + m)
             x = make_x(m, k, seed=k + 3)
             tw = pkg.upload(qtype, blocks, n, k, device=cuda)
