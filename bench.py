@@ -157,38 +157,51 @@ SWEEP_SHAPES = [("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584),
                 ("down", 3584, 18944)]
 
 
-def bench_sweep(pkg, torch, steps, warmup, fused):
+def bench_sweep(pkg, torch, steps, warmup, mode):
     """28 layers x {q,k,v,o,gate,up,down} q4_0 GEMVs (hidden 3584, FFN 18944,
     GQA kv 512), M = 1, one fixed x per input size, one graph = one decode
-    step. fused=True uploads q|k|v and gate|up as concatenated weights (each
-    pair/triple shares its input), so a layer is 4 launches instead of 7;
-    the bytes and flops are the same."""
+    step. mode "fused" uploads q|k|v and gate|up as concatenated weights
+    (each pair/triple shares its input), so a layer is 4 launches instead
+    of 7; "epilogue" also adds the q|k|v bias in the kernel (Qwen2 has one)
+    and interleaves gate|up for the SwiGLU epilogue, which writes
+    silu(gate) * up (18944 floats instead of 2 x 18944) — the decode step's
+    Linear work with no separate bias, SiLU or multiply launch. The weight
+    bytes and flops are the same in every mode."""
     import mini_llama_amd.synth as synth
     xs = {kk: torch.from_numpy(synth.make_x(1, kk, 900 + kk)[0]).to("cuda")
           for kk in (3584, 18944)}
-    log(f"sweep ({'fused' if fused else '196 launches'}): uploading 28 layers")
+    log(f"sweep ({mode}): uploading 28 layers")
     calls = []
     for layer in range(28):
         blk = {name: (synth.make_blocks("q4_0", n, k, 5000 + 10 * layer + i), n, k)
                for i, (name, n, k) in enumerate(SWEEP_SHAPES)}
-        if fused:
-            groups = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
-        else:
+        if mode == "separate":
             groups = [[name] for name, _, _ in SWEEP_SHAPES]
+        else:
+            groups = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
         for g in groups:
             k = blk[g[0]][2]
+            bias, act = None, pkg.EPI_NONE
             if len(g) == 1:
                 w = pkg.upload("q4_0", blk[g[0]][0], blk[g[0]][1], k, device="cuda")
+            elif mode == "epilogue" and g[0] == "gate":
+                ffn = blk["gate"][1]
+                w = pkg.upload_glu("q4_0", blk["gate"][0], blk["up"][0], ffn, k,
+                                   device="cuda")
+                act = pkg.EPI_SWIGLU
             else:
                 w, _ = pkg.upload_concat("q4_0", [(blk[nm][0], blk[nm][1]) for nm in g],
                                          k, device="cuda")
-            y = torch.empty(w.n, dtype=torch.float32, device="cuda")
-            calls.append((w, xs[k], y))
+                if mode == "epilogue":
+                    bias = torch.from_numpy(synth.make_x(1, w.n, 77 + layer)[0]).to("cuda")
+            ny = w.n // 2 if act == pkg.EPI_SWIGLU else w.n
+            y = torch.empty(ny, dtype=torch.float32, device="cuda")
+            calls.append((w, xs[k], y, bias, act))
     del blk
 
     def step(_):
-        for w, x, y in calls:
-            pkg.linear(w, x, y)
+        for w, x, y, bias, act in calls:
+            pkg.linear(w, x, y, bias=bias, act=act)
 
     steps = max(1, steps)
     sec = time_graph(torch, step, steps, warmup) / steps
@@ -309,11 +322,12 @@ def main():
             extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
                            for kk, v in r.items()}
             extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
-        for fused in (False, True):
-            sw = bench_sweep(pkg, torch, max(1, args.steps // 100), 1, fused)
+        for mode, key in (("separate", "sweep"), ("fused", "sweep_fused"),
+                          ("epilogue", "sweep_epilogue")):
+            sw = bench_sweep(pkg, torch, max(1, args.steps // 100), 1, mode)
             sw["frac_hbm"] = round(sw["gbs"] / HBM_PEAK_GBS, 4)
-            extra["sweep_fused" if fused else "sweep"] = {
-                kk: (round(v, 3) if isinstance(v, float) else v) for kk, v in sw.items()}
+            extra[key] = {kk: (round(v, 3) if isinstance(v, float) else v)
+                          for kk, v in sw.items()}
         result["configs"] = extra
     if not args.no_cpu:
         log("cpu baseline")

@@ -152,6 +152,31 @@ int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes);
 int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
                   void* workspace, size_t workspace_bytes, mlq_stream_t stream);
 
+/* Output epilogues of mlq_linear_epi. */
+enum mlq_epilogue { MLQ_EPI_NONE = 0, MLQ_EPI_SWIGLU = 1 };
+
+/* mlq_linear_ws with a fused output epilogue (no counterpart in the
+ * reference, which runs the bias add and SwiGLU as separate ops:
+ * src/forward.cc:383-416 bias, 361-370 silu(gate) * up). bias[n] (device,
+ * may be NULL) is added to every output row. MLQ_EPI_SWIGLU: w is a gate
+ * and an up projection of `ffn` = n/2 rows each, interleaved with
+ * mlq_interleave_rows (n % 16 == 0, else MLQ_ERR_SHAPE; bias interleaved
+ * the same way); y is [m][n/2] with y[r][i] = silu(gate_i + bias) *
+ * (up_i + bias), silu(g) = g / (1 + exp(-g)) in fp32. Workspace and
+ * result contract as mlq_linear_ws (the decode GEMV, m <= 8, needs none). */
+int mlq_linear_epi(const mlq_weight* w, const float* x, float* y, int m,
+                   const float* bias, int act, void* workspace,
+                   size_t workspace_bytes, mlq_stream_t stream);
+
+/* Host helper for MLQ_EPI_SWIGLU weights: interleave `rows` rows of a gate
+ * and an up matrix (any row format of row_bytes bytes: GGUF block rows
+ * before repacking, or fp32 bias entries) into out (2 * rows rows): rows
+ * 16t..16t+7 of out are gate rows 8t..8t+7, rows 16t+8..16t+15 up rows
+ * 8t..8t+7. rows % 8 == 0, else MLQ_ERR_SHAPE. No counterpart in the
+ * reference (it keeps ffn_gate and ffn_up as separate tensors). */
+int mlq_interleave_rows(const void* gate, const void* up, int rows,
+                        size_t row_bytes, void* out);
+
 /* Raw GGUF AoS blocks in device memory: the meaning of the `const void*`
  * weight of cudaQ*LinearDeviceWeight / cudaQ*LinearDeviceInput
  * (src/cuda_quant.cu:300-361). The blocks are repacked into `workspace`

@@ -27,6 +27,7 @@ TYPES = {"q8_0": Q8_0, "q4_0": Q4_0, "q4_1": Q4_1}
 BLOCK_BYTES = {"q8_0": 34, "q4_0": 18, "q4_1": 20}
 # enum mlq_path
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
+EPI_NONE, EPI_SWIGLU = 0, 1
 GEMV_MAX_ROWS = 8
 
 STATUS = {
@@ -78,6 +79,8 @@ SIGNATURES = {
     "mlq_linear_path": ([_WP, _P, _P, _I, _I, _P], _I),
     "mlq_linear_workspace": ([_WP, _I, ctypes.POINTER(_Z)], _I),
     "mlq_linear_ws": ([_WP, _P, _P, _I, _P, _Z, _P], _I),
+    "mlq_linear_epi": ([_WP, _P, _P, _I, _P, _I, _P, _Z, _P], _I),
+    "mlq_interleave_rows": ([_P, _P, _I, _Z, _P], _I),
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
     "mlq_set_gemv_split": ([_I], _I),
     "mlq_set_gemm_split": ([_I], _I),
@@ -192,6 +195,30 @@ def upload_concat(qtype: str, parts, k: int, device: str = "cuda"):
     return upload(qtype, blocks, offsets[-1], k, device=device), offsets
 
 
+def interleave_rows(gate: np.ndarray, up: np.ndarray, rows: int) -> np.ndarray:
+    """Rows of gate and up interleaved per 16-row tile (8 gate rows, then
+    the matching 8 up rows) by mlq_interleave_rows; any row format (GGUF
+    block rows, fp32 bias entries)."""
+    g = np.ascontiguousarray(gate).view(np.uint8).reshape(-1)
+    u = np.ascontiguousarray(up).view(np.uint8).reshape(-1)
+    if g.size != u.size or g.size % rows:
+        raise ValueError("gate and up must hold `rows` rows of equal size")
+    out = np.empty(2 * g.size, dtype=np.uint8)
+    _check(lib().mlq_interleave_rows(g.ctypes.data, u.ctypes.data, rows,
+                                     g.size // rows, out.ctypes.data),
+           "mlq_interleave_rows")
+    return out.view(np.asarray(gate).dtype)
+
+
+def upload_glu(qtype: str, gate_blocks, up_blocks, ffn: int, k: int,
+               device: str = "cuda") -> TiledWeight:
+    """Gate and up projections [ffn, k] as one tiled weight of 2*ffn rows
+    for act=EPI_SWIGLU (ffn % 8 == 0): one launch reads x once and writes
+    silu(gate) * up."""
+    return upload(qtype, interleave_rows(gate_blocks, up_blocks, ffn),
+                  2 * ffn, k, device=device)
+
+
 def upload_aos(blocks: np.ndarray, device: str = "cuda"):
     """Raw GGUF blocks to device memory unchanged (what the reference uploads)."""
     import torch
@@ -249,12 +276,14 @@ def _workspace(device, nbytes: int):
 
 
 def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None,
-           workspace="auto"):
+           workspace="auto", bias=None, act: int = EPI_NONE):
     """y[m, n] = x[m, k] @ W^T on the device (x fp32 contiguous, 1-D or 2-D).
 
     path AUTO with a workspace (the default "auto" takes the per-device one)
-    runs mlq_linear_ws; workspace=None, or a forced path, runs
-    mlq_linear_path (the prefill GEMM then reads fp32 x directly)."""
+    runs mlq_linear_epi: optional fused bias (fp32 device tensor [n]) and
+    act=EPI_SWIGLU for a weight made by upload_glu (y then has n/2
+    columns). workspace=None, or a forced path, runs mlq_linear_path (no
+    epilogue; the prefill GEMM then reads fp32 x directly)."""
     import torch
     if x.dtype != torch.float32 or not x.is_contiguous():
         raise ValueError("x must be a contiguous float32 device tensor")
@@ -262,8 +291,14 @@ def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None,
     kx = x.shape[-1]
     if kx != w.k:
         raise ValueError(f"in_features mismatch: x has {kx}, weight has {w.k}")
+    fused = bias is not None or act != EPI_NONE
+    if fused and (path != PATH_AUTO or workspace is None):
+        raise ValueError("bias / act need the default path with a workspace")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != w.n):
+        raise ValueError(f"bias must be float32 with {w.n} elements")
+    ny = w.n // 2 if act == EPI_SWIGLU else w.n
     if y is None:
-        shape = (w.n,) if x.dim() == 1 else (m, w.n)
+        shape = (ny,) if x.dim() == 1 else (m, ny)
         y = torch.empty(shape, dtype=torch.float32, device=x.device)
     if path == PATH_AUTO and workspace is not None:
         need = workspace_bytes(w, m)
@@ -272,9 +307,11 @@ def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None,
             ws = _workspace(x.device, need) if need else None
         ws_ptr = ws.data_ptr() if ws is not None else None
         ws_len = ws.numel() * ws.element_size() if ws is not None else 0
-        _check(lib().mlq_linear_ws(ctypes.byref(w.layout), x.data_ptr(),
-                                   y.data_ptr(), m, ws_ptr, ws_len,
-                                   _stream(stream)), "mlq_linear_ws")
+        _check(lib().mlq_linear_epi(ctypes.byref(w.layout), x.data_ptr(),
+                                    y.data_ptr(), m,
+                                    bias.data_ptr() if bias is not None else None,
+                                    act, ws_ptr, ws_len, _stream(stream)),
+               "mlq_linear_epi")
         return y
     _check(lib().mlq_linear_path(ctypes.byref(w.layout), x.data_ptr(),
                                  y.data_ptr(), m, path, _stream(stream)),

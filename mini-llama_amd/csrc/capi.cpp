@@ -212,15 +212,20 @@ int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes) {
   return MLQ_OK;
 }
 
-int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
-                  void* workspace, size_t workspace_bytes,
-                  mlq_stream_t stream) {
+int mlq_linear_epi(const mlq_weight* w, const float* x, float* y, int m,
+                   const float* bias, int act, void* workspace,
+                   size_t workspace_bytes, mlq_stream_t stream) {
   int rc = check_tiled(w);
   if (rc != MLQ_OK) return rc;
   if (x == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
+  if (act != MLQ_EPI_NONE && act != MLQ_EPI_SWIGLU) return MLQ_ERR_INVALID_ARG;
+  if (act == MLQ_EPI_SWIGLU && w->n % 16 != 0) return MLQ_ERR_SHAPE;
+  Epilogue epi;
+  epi.bias = bias;
+  epi.act = act == MLQ_EPI_SWIGLU ? kEpiSwiGLU : kEpiNone;
   const hipStream_t s = (hipStream_t)stream;
-  if (uses_gemv(w, m)) return hip_status(launch_gemv(*w, x, y, m, s));
+  if (uses_gemv(w, m)) return hip_status(launch_gemv(*w, x, y, m, s, epi));
   const size_t need = m <= kSkinnyMaxRows ? skinny_x_bytes(m, w->k)
                                            : gemm_workspace_bytes(m, w->n, w->k);
   if (workspace == nullptr || workspace_bytes < need)
@@ -231,9 +236,33 @@ int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
     _Float16* xf = (_Float16*)workspace;
     rc = hip_status(launch_x_to_frag(x, xf, m, w->k, s));
     if (rc != MLQ_OK) return rc;
-    return hip_status(launch_skinny(*w, xf, y, m, s));
+    return hip_status(launch_skinny(*w, xf, y, m, s, epi));
   }
-  return hip_status(launch_gemm_ws(*w, x, y, m, workspace, workspace_bytes, s));
+  return hip_status(launch_gemm_ws(*w, x, y, m, workspace, workspace_bytes, s, epi));
+}
+
+int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
+                  void* workspace, size_t workspace_bytes,
+                  mlq_stream_t stream) {
+  return mlq_linear_epi(w, x, y, m, nullptr, MLQ_EPI_NONE, workspace,
+                        workspace_bytes, stream);
+}
+
+int mlq_interleave_rows(const void* gate, const void* up, int rows,
+                        size_t row_bytes, void* out) {
+  if (gate == nullptr || up == nullptr || out == nullptr || row_bytes == 0)
+    return MLQ_ERR_INVALID_ARG;
+  if (rows <= 0 || rows % 8 != 0) return MLQ_ERR_SHAPE;
+  const uint8_t* g = (const uint8_t*)gate;
+  const uint8_t* u = (const uint8_t*)up;
+  uint8_t* o = (uint8_t*)out;
+  // output rows 16t + c = gate row 8t + c, 16t + 8 + c = up row 8t + c
+  for (int t = 0; t < rows / 8; ++t) {
+    std::memcpy(o + (size_t)16 * t * row_bytes, g + (size_t)8 * t * row_bytes, 8 * row_bytes);
+    std::memcpy(o + (size_t)(16 * t + 8) * row_bytes, u + (size_t)8 * t * row_bytes,
+                8 * row_bytes);
+  }
+  return MLQ_OK;
 }
 
 int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,

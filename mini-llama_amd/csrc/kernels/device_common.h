@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "launch.h"
+
 namespace mlq {
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
@@ -117,6 +119,16 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   h.x = (_Float16)a;
   h.y = (_Float16)b;
   return as_u32(h);
+}
+
+// ---- output epilogue (Epilogue, kEpi* in launch.h) ---------------------------
+// silu in fp32 with the hardware exp (v_exp_f32 on g * log2(e)): within a
+// few ulp of g / (1 + expf(-g))
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+// output column of gate row `row` (row % 16 < 8) under kEpiSwiGLU
+__device__ __forceinline__ int glu_col(int row) { return (row >> 4) * 8 + (row & 7); }
+__device__ __forceinline__ float add_bias(const Epilogue& e, float v, int row) {
+  return e.bias != nullptr ? v + e.bias[row] : v;
 }
 
 }  // namespace mlq

@@ -64,6 +64,8 @@ struct GemmArgs {
   int kp;              // row stride of xh: k rounded up to whole stages
   int mtiles, ntiles;  // output tiles
   int splits;          // K ranges per output tile (workgroups per tile)
+  Epilogue epi;        // applied here when splits == 1, else by the reduce
+  int ny;              // output columns: n, or n/2 under kEpiSwiGLU
 };
 
 // Activation source: fp32 rows loaded as float4 (k % 4 == 0), fp32 loaded
@@ -386,43 +388,108 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(GemmArgs a) {
   if (s + 4 <= stages) { step(s + 2, Slot<2>{}); step(s + 3, Slot<3>{}); }
 
   // epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each
-  // 32x32 block; with several K ranges each writes its own partial slice
-  float* out = a.splits > 1 ? a.part + (size_t)sp * a.m * a.n : a.y;
+  // 32x32 block; with several K ranges each writes its own raw partial
+  // slice and the reduce applies the epilogue
+  if (a.splits > 1) {
+    float* out = a.part + (size_t)sp * a.m * a.n;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ncol = tile0 * kTileRows + 64 * wn + 32 * j + fr;
+        if (ncol >= a.n) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int mrow = m0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (mrow < a.m) out[(size_t)mrow * a.n + ncol] = acc[i][j][r];
+        }
+      }
+    }
+    return;
+  }
+  // one code path per (bias, SwiGLU) choice: no per-element branches; the
+  // bias depends on the column only, so a lane loads it once per block
+  auto store = [&](auto bias_c, auto glu_c) {
+    constexpr bool HB = decltype(bias_c)::v, GL = decltype(glu_c)::v;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int ncol = tile0 * kTileRows + 64 * wn + 32 * j + fr;
-      if (ncol >= a.n) continue;
+      const float bj = HB ? a.epi.bias[min(ncol, a.n - 1)] : 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int mrow = m0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (mrow < a.m) out[(size_t)mrow * a.n + ncol] = acc[i][j][r];
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int mrow = m0 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const float v = HB ? acc[i][j][r] + bj : acc[i][j][r];
+          if (GL) {
+            // the up row of column ncol (ncol % 16 < 8) is in lane ^ 8
+            const float u = __shfl_xor(v, 8);
+            if ((fr & 8) == 0 && ncol < a.n && mrow < a.m)
+              a.y[(size_t)mrow * a.ny + glu_col(ncol)] = silu_f(v) * u;
+          } else if (ncol < a.n && mrow < a.m) {
+            a.y[(size_t)mrow * a.n + ncol] = v;
+          }
+        }
       }
     }
+  };
+  const bool hb = a.epi.bias != nullptr;
+  if (a.epi.act == kEpiSwiGLU) {
+    if (hb) store(Slot<1>{}, Slot<1>{});
+    else store(Slot<0>{}, Slot<1>{});
+  } else {
+    if (hb) store(Slot<1>{}, Slot<0>{});
+    else store(Slot<0>{}, Slot<0>{});
   }
 }
 
-// y = sum of the split-K partial slices, in slice order (deterministic).
-// VEC: count % 4 == 0, four outputs per thread.
+// y = epilogue(sum of the split-K partial slices, in slice order:
+// deterministic). One thread per four consecutive outputs of a row when
+// VEC (n % 4 == 0), else per output.
 template <bool VEC>
-__global__ __launch_bounds__(256) void split_reduce_kernel(const float* part,
-                                                           float* y,
-                                                           size_t count,
-                                                           int splits) {
-  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * (VEC ? 4 : 1);
-  if (i >= count) return;
-  if (VEC) {
-    float4 s = *(const float4*)(part + i);
-    for (int p = 1; p < splits; ++p) {
-      const float4 v = *(const float4*)(part + (size_t)p * count + i);
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, float* y,
+                                                           int m, int n, int splits,
+                                                           Epilogue epi, int ny) {
+  constexpr int V = VEC ? 4 : 1;
+  const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
+  if (o >= (size_t)m * ny) return;
+  const int r = (int)(o / ny), c = (int)(o % ny);
+  const size_t count = (size_t)m * n;
+  auto sum = [&](int col, float (&s)[V]) {
+    const float* p0 = part + (size_t)r * n + col;
+    if (VEC) {
+      float4 t = *(const float4*)p0;
+      for (int p = 1; p < splits; ++p) {
+        const float4 v = *(const float4*)(p0 + (size_t)p * count);
+        t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+      }
+      s[0] = t.x; s[V > 1 ? 1 : 0] = t.y; s[V > 2 ? 2 : 0] = t.z; s[V > 3 ? 3 : 0] = t.w;
+    } else {
+      float t = p0[0];
+      for (int p = 1; p < splits; ++p) t += p0[(size_t)p * count];
+      s[0] = t;
     }
-    *(float4*)(y + i) = s;
+  };
+  float out[V];
+  if (epi.act == kEpiSwiGLU) {
+    // output column c -> gate row 16(c/8) + c%8, up row + 8
+    const int row = 16 * (c / 8) + c % 8;
+    float g[V], u[V];
+    sum(row, g);
+    sum(row + 8, u);
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      out[e] = silu_f(add_bias(epi, g[e], row + e)) * add_bias(epi, u[e], row + 8 + e);
   } else {
-    float s = part[i];
-    for (int p = 1; p < splits; ++p) s += part[(size_t)p * count + i];
-    y[i] = s;
+    float s[V];
+    sum(c, s);
+#pragma unroll
+    for (int e = 0; e < V; ++e) out[e] = add_bias(epi, s[e], c + e);
+  }
+  if (VEC) {
+    *(float4*)(y + o) = make_float4(out[0], out[V > 1 ? 1 : 0], out[V > 2 ? 2 : 0], out[V > 3 ? 3 : 0]);
+  } else {
+    y[o] = out[0];
   }
 }
 
@@ -464,14 +531,14 @@ hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
-  const size_t count = (size_t)a.m * a.n;
-  if (count % 4 == 0) {
-    const size_t threads = count / 4;
+  const size_t outs = (size_t)a.m * a.ny;
+  if (a.n % 4 == 0) {
+    const size_t threads = outs / 4;
     split_reduce_kernel<true><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
-        a.part, a.y, count, a.splits);
+        a.part, a.y, a.m, a.n, a.splits, a.epi, a.ny);
   } else {
-    split_reduce_kernel<false><<<(unsigned)((count + 255) / 256), 256, 0, stream>>>(
-        a.part, a.y, count, a.splits);
+    split_reduce_kernel<false><<<(unsigned)((outs + 255) / 256), 256, 0, stream>>>(
+        a.part, a.y, a.m, a.n, a.splits, a.epi, a.ny);
   }
   return hipGetLastError();
 }
@@ -551,7 +618,8 @@ hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
 }
 
 hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
-                          void* ws, size_t ws_bytes, hipStream_t stream) {
+                          void* ws, size_t ws_bytes, hipStream_t stream,
+                          const Epilogue& epi) {
   const Geometry geo = geometry(w.n, w.k);
   GemmArgs a;
   a.qs = (const uint8_t*)w.base + w.qs_off;
@@ -570,6 +638,8 @@ hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
   a.ntiles = (geo.nt + kTiles - 1) / kTiles;
   a.splits = 1;
   a.part = nullptr;
+  a.epi = epi;
+  a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
   // every activation row offset of a workgroup must fit a 32-bit buffer
   // offset
   if ((size_t)kBM * (size_t)w.k * 4 >= (1ull << 31)) return hipErrorInvalidValue;

@@ -78,6 +78,8 @@ struct GemvArgs {
   int gw;        // groups per wave (the last slice may be shorter)
   int xstride;   // fp16 elements per staged activation row
   int wave_lds;  // bytes of LDS per wave (activation slice + block sums)
+  Epilogue epi;
+  int ny;        // output columns: n, or n/2 under kEpiSwiGLU
 };
 
 template <int QT>
@@ -362,9 +364,21 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // ---- output ------------------------------------------------------------
   if (a.split == 1) {
     const int row = tile * kTileRows + n;
+    const float v0 = add_bias(a.epi, acc0, min(row, a.n - 1));
+    const float v1 = add_bias(a.epi, acc1, min(row, a.n - 1));
+    if (a.epi.act == kEpiSwiGLU) {
+      // the up row of lane n (< 8) sits in lane n + 8
+      const float u0 = __shfl_xor(v0, 8);
+      const float u1 = __shfl_xor(v1, 8);
+      if (n < 8 && row < a.n) {
+        if (r0 < M) a.y[(size_t)r0 * a.ny + glu_col(row)] = silu_f(v0) * u0;
+        if (MR > 1 && r1 < M) a.y[(size_t)r1 * a.ny + glu_col(row)] = silu_f(v1) * u1;
+      }
+      return;
+    }
     if (row < a.n) {
-      if (r0 < M) a.y[(size_t)r0 * a.n + row] = acc0;
-      if (MR > 1 && r1 < M) a.y[(size_t)r1 * a.n + row] = acc1;
+      if (r0 < M) a.y[(size_t)r0 * a.n + row] = v0;
+      if (MR > 1 && r1 < M) a.y[(size_t)r1 * a.n + row] = v1;
     }
     return;
   }
@@ -372,12 +386,26 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   if (r0 < M) part[(wave * M + r0) * kTileRows + n] = acc0;
   if (MR > 1 && r1 < M) part[(wave * M + r1) * kTileRows + n] = acc1;
   __syncthreads();
-  for (int o = tid; o < M * kTileRows; o += blockDim.x) {
-    const int r = o / kTileRows, nn = o % kTileRows;
+  auto slice_sum = [&](int r, int nn) {
     float s = 0.0f;
     for (int w = 0; w < a.split; ++w) s += part[(w * M + r) * kTileRows + nn];
+    return s;
+  };
+  if (a.epi.act == kEpiSwiGLU) {
+    for (int o = tid; o < M * 8; o += blockDim.x) {
+      const int r = o / 8, c = o % 8;
+      const int row = tile * kTileRows + c;
+      if (row >= a.n) continue;
+      const float g = add_bias(a.epi, slice_sum(r, c), row);
+      const float u = add_bias(a.epi, slice_sum(r, c + 8), row + 8);
+      a.y[(size_t)r * a.ny + glu_col(row)] = silu_f(g) * u;
+    }
+    return;
+  }
+  for (int o = tid; o < M * kTileRows; o += blockDim.x) {
+    const int r = o / kTileRows, nn = o % kTileRows;
     const int row = tile * kTileRows + nn;
-    if (row < a.n) a.y[(size_t)r * a.n + row] = s;
+    if (row < a.n) a.y[(size_t)r * a.n + row] = add_bias(a.epi, slice_sum(r, nn), row);
   }
 }
 
@@ -566,7 +594,7 @@ int gemv_max_k(int type, int m) {
 }
 
 hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
-                       hipStream_t stream) {
+                       hipStream_t stream, const Epilogue& epi) {
   const Geometry geo = geometry(w.n, w.k);
   if (m < 1 || m > kGemvMaxRows) return hipErrorInvalidValue;
   const Plan p = make_plan(w.type, m, geo);
@@ -586,6 +614,8 @@ hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
   a.gw = p.gw;
   a.xstride = p.padded * kGroupK + kRowPadHalves;
   a.wave_lds = (int)p.wave_lds;
+  a.epi = epi;
+  a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
   switch (w.type) {
     case MLQ_Q8_0: return launch_rows<MLQ_Q8_0>(a, p, stream);
     case MLQ_Q4_0: return launch_rows<MLQ_Q4_0>(a, p, stream);

@@ -8,6 +8,21 @@
 
 namespace mlq {
 
+// Output epilogue of the Linear kernels: they store act(acc + bias[row]) for
+// output row `row` of W.
+//  kEpiNone:   y[r][row] = acc + bias[row] (bias optional).
+//  kEpiSwiGLU: W holds a gate and an up projection interleaved per 16-row
+//              tile (rows 16t..16t+7 are gate rows 8t..8t+7, rows
+//              16t+8..16t+15 the matching up rows); y has n/2 columns and
+//              y[r][8t + c] = silu(gate + bias) * (up + bias) with
+//              silu(g) = g / (1 + exp(-g)) in fp32 (the reference's SiLU and
+//              elementwise product, src/forward.cc:361-370).
+enum { kEpiNone = 0, kEpiSwiGLU = 1 };
+struct Epilogue {
+  const float* bias = nullptr;  // [n] or nullptr
+  int act = kEpiNone;
+};
+
 // repack.hip
 hipError_t launch_repack(int type, const void* aos, int n, int k,
                          const mlq_weight& w, hipStream_t stream);
@@ -20,7 +35,7 @@ hipError_t launch_bias(float* y, const float* bias, int m, int n,
 constexpr int kGemvMaxRows = 8;
 // Returns hipErrorInvalidValue when the activation staging does not fit LDS.
 hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
-                       hipStream_t stream);
+                       hipStream_t stream, const Epilogue& epi = Epilogue());
 // Largest k the GEMV accepts for m rows (LDS-bound).
 int gemv_max_k(int type, int m);
 // Split override (0 = automatic); validated by the caller.
@@ -34,7 +49,8 @@ void set_gemv_split(int split);
 hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream);
 hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
-                          void* ws, size_t ws_bytes, hipStream_t stream);
+                          void* ws, size_t ws_bytes, hipStream_t stream,
+                          const Epilogue& epi = Epilogue());
 size_t f16_copy_bytes(int m, int k);
 int gemm_splits(int m, int n, int k);
 size_t gemm_workspace_bytes(int m, int n, int k);
@@ -52,6 +68,6 @@ size_t skinny_x_bytes(int m, int k);
 hipError_t launch_x_to_frag(const float* x, _Float16* xf, int m, int k,
                             hipStream_t stream);
 hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int m,
-                         hipStream_t stream);
+                         hipStream_t stream, const Epilogue& epi = Epilogue());
 
 }  // namespace mlq

@@ -42,6 +42,8 @@ struct SkinnyArgs {
   const _Float16* xf;  // fragment-ordered fp16 copy of x (skinny_x_bytes)
   float* y;
   int m, n, g, nt;
+  Epilogue epi;
+  int ny;              // output columns: n, or n/2 under kEpiSwiGLU
 };
 
 // One 128-k group of T weight tiles and the x fragments of all row blocks.
@@ -192,13 +194,27 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyArgs a) {
       for (int i = 0; i < 4; ++i)
         part[(wave * 64 + 16 * mb + rq4 + i) * 16 + col] = acc[t][mb][i];
     __syncthreads();
-    for (int o = tid; o < a.m * 16; o += kThreads) {
-      const int r = o / 16, c = o % 16;
+    auto wave_sum = [&](int r, int c) {
       float s = 0.0f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) s += part[(w * 64 + r) * 16 + c];
-      const int row = (t0 + t) * kTileRows + c;
-      if (row < a.n) a.y[(size_t)r * a.n + row] = s;
+      return s;
+    };
+    if (a.epi.act == kEpiSwiGLU) {
+      for (int o = tid; o < a.m * 8; o += kThreads) {
+        const int r = o / 8, c = o % 8;
+        const int row = (t0 + t) * kTileRows + c;
+        if (row >= a.n) continue;
+        const float g = add_bias(a.epi, wave_sum(r, c), row);
+        const float u = add_bias(a.epi, wave_sum(r, c + 8), row + 8);
+        a.y[(size_t)r * a.ny + glu_col(row)] = silu_f(g) * u;
+      }
+    } else {
+      for (int o = tid; o < a.m * 16; o += kThreads) {
+        const int r = o / 16, c = o % 16;
+        const int row = (t0 + t) * kTileRows + c;
+        if (row < a.n) a.y[(size_t)r * a.n + row] = add_bias(a.epi, wave_sum(r, c), row);
+      }
     }
     if (t + 1 < T) __syncthreads();
   }
@@ -283,7 +299,7 @@ hipError_t launch_x_to_frag(const float* x, _Float16* xf, int m, int k,
 }
 
 hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int m,
-                         hipStream_t stream) {
+                         hipStream_t stream, const Epilogue& epi) {
   if (m < 1 || m > kSkinnyMaxRows) return hipErrorInvalidValue;
   // 32-bit buffer offsets for the x fragments of a wave
   if (skinny_x_bytes(m, w.k) >= (1ull << 31)) return hipErrorInvalidValue;
@@ -298,6 +314,8 @@ hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int 
   a.n = w.n;
   a.g = geo.g;
   a.nt = geo.nt;
+  a.epi = epi;
+  a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
   switch (w.type) {
     case MLQ_Q8_0: return launch_typed<MLQ_Q8_0>(a, stream);
     case MLQ_Q4_0: return launch_typed<MLQ_Q4_0>(a, stream);

@@ -178,6 +178,35 @@ def test_linear_validation_without_device(pkg):
     assert lib.mlq_dequantize(None, 0, 1, 1, None) == -1
 
 
+def test_epilogue_validation_without_device(pkg):
+    """mlq_linear_epi rejects unknown epilogues and SwiGLU on weights whose
+    row count is not a whole number of 16-row gate/up tiles."""
+    lib = pkg.lib()
+    w = pkg.weight_layout("q4_0", 40, 64)
+    w.base = 1
+    assert lib.mlq_linear_epi(ctypes.byref(w), 1, 1, 1, None, 7, None, 0, None) == -1
+    assert lib.mlq_linear_epi(ctypes.byref(w), 1, 1, 1, None, pkg.EPI_SWIGLU, None, 0, None) == -2
+    assert lib.mlq_linear_epi(ctypes.byref(w), None, 1, 1, None, 0, None, 0, None) == -1
+
+
+def test_interleave_rows_permutation(pkg):
+    """Rows 16t..16t+7 of the result are gate rows 8t..8t+7 and rows
+    16t+8..16t+15 the matching up rows, for any row size."""
+    rng = np.random.default_rng(3)
+    for rows, row_bytes in [(8, 1), (24, 18 * 3), (64, 4)]:
+        gate = rng.integers(0, 256, size=(rows, row_bytes), dtype=np.uint8)
+        up = rng.integers(0, 256, size=(rows, row_bytes), dtype=np.uint8)
+        out = pkg.interleave_rows(gate, up, rows).reshape(2 * rows, row_bytes)
+        for t in range(rows // 8):
+            assert np.array_equal(out[16 * t:16 * t + 8], gate[8 * t:8 * t + 8])
+            assert np.array_equal(out[16 * t + 8:16 * t + 16], up[8 * t:8 * t + 8])
+    lib = pkg.lib()
+    buf = np.zeros(64, dtype=np.uint8)
+    assert lib.mlq_interleave_rows(buf.ctypes.data, buf.ctypes.data, 12, 1,
+                                   buf.ctypes.data) == -2
+    assert lib.mlq_interleave_rows(None, buf.ctypes.data, 8, 1, buf.ctypes.data) == -1
+
+
 def test_cpp_binary_runs_host_checks(pkg):
     """The C++ suite on a host without a GPU: device tests skip, backend
     parsing/validation runs."""

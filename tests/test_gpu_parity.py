@@ -300,6 +300,69 @@ def test_gemm_every_split(pkg, oracle, cuda, qtype, split):
         pkg.set_gemm_split(0)
 
 
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("m,n,k", [(1, 48, 128), (1, 300, 1001), (4, 64, 512),
+                                   (16, 8200, 256), (40, 100, 300), (130, 70, 300),
+                                   (300, 272, 640), (512, 2048, 256)])
+def test_fused_bias_matches_separate_add(pkg, cuda, qtype, m, n, k):
+    """The bias added in every kernel's epilogue (GEMV with one and several
+    K slices, skinny, split-K reduce, prefill GEMM) equals the kernel output
+    plus the bias, bit for bit: the same single fp32 addition."""
+    torch = _torch()
+    _print_case(test="bias", qtype=qtype, m=m, n=n, k=k)
+    blocks = make_blocks(qtype, n, k, seed=m + n + 2 * k)
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    x = make_x(m, k, seed=k + 11)
+    xd = _dev(x if m > 1 else x[0], cuda)
+    bias = torch.from_numpy(make_x(1, n, seed=n)[0]).to(cuda)
+    plain = pkg.linear(tw, xd)
+    fused = pkg.linear(tw, xd, bias=bias)
+    assert torch.equal(fused, plain + bias)
+
+
+def _silu64(g):
+    return g / (1.0 + np.exp(-g))
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("m,ffn,k", [(1, 48, 128), (1, 520, 1001), (4, 64, 512),
+                                     (16, 4104, 256), (40, 56, 300), (130, 40, 300),
+                                     (300, 136, 640), (512, 1024, 256)])
+def test_fused_swiglu(pkg, oracle, cuda, qtype, m, ffn, k):
+    """gate|up interleaved (upload_glu) with the SwiGLU epilogue: the same
+    pre-activations as two separate launches (bit for bit), silu(g) * u in
+    fp32 within 1e-5 of the float64 formula on them, and within the stated
+    tolerance of the oracle (propagated: |silu'| <= 1.1)."""
+    torch = _torch()
+    _print_case(test="swiglu", qtype=qtype, m=m, ffn=ffn, k=k)
+    gate = make_blocks(qtype, ffn, k, seed=ffn + k)
+    up = make_blocks(qtype, ffn, k, seed=ffn + k + 1)
+    x = make_x(m, k, seed=k + 5)
+    xd = _dev(x if m > 1 else x[0], cuda)
+    bg = make_x(1, ffn, seed=ffn + 2)[0]
+    bu = make_x(1, ffn, seed=ffn + 3)[0]
+    tw = pkg.upload_glu(qtype, gate, up, ffn, k, device=cuda)
+    bias = torch.from_numpy(pkg.interleave_rows(bg, bu, ffn)).to(cuda)
+    got = np.atleast_2d(pkg.linear(tw, xd, bias=bias, act=pkg.EPI_SWIGLU).cpu().numpy())
+    assert got.shape == (m, ffn)
+    # pre-activations from separate launches of the same kernels
+    tg = pkg.upload(qtype, gate, ffn, k, device=cuda)
+    tu = pkg.upload(qtype, up, ffn, k, device=cuda)
+    g = np.atleast_2d(pkg.linear(tg, xd).cpu().numpy()).astype(np.float64) + bg
+    u = np.atleast_2d(pkg.linear(tu, xd).cpu().numpy()).astype(np.float64) + bu
+    ref = _silu64(g) * u
+    scale = np.abs(ref).max() + 1e-30
+    assert np.abs(got - ref).max() <= 1e-5 * scale, np.abs(got - ref).max() / scale
+    # against the oracle
+    go = oracle.linear(x, gate, (ffn, k), qtype).astype(np.float64) + bg
+    uo = oracle.linear(x, up, (ffn, k), qtype).astype(np.float64) + bu
+    ro = _silu64(go) * uo
+    atol = 1e-3 * np.linalg.norm(x, axis=1, keepdims=True) * np.sqrt(k / 4096)
+    bound = (1.1 * np.abs(uo) + np.abs(_silu64(go))) * atol + 1.1 * atol * atol
+    err = np.abs(got - ro)
+    assert np.all((err <= bound) | (err <= 2e-3 * np.abs(ro))), err.max()
+
+
 @pytest.mark.parametrize("m", [1, 3, 16])
 def test_concatenated_weights_match_separate(pkg, oracle, cuda, m):
     """q|k|v-style fusion: one tiled weight holding several weights' rows
