@@ -214,6 +214,56 @@ def bench_sweep(pkg, torch, steps, warmup, mode):
             "gbs": total / sec / 1e9, "bytes": total, "tflops": flops / sec / 1e12}
 
 
+def bench_gguf_load(pkg, torch, layers=4):
+    """Weight load from a GGUF file: `layers` Qwen2-7B layers (q4_0, 7
+    Linear tensors each, ~131 MB per layer) written to a temporary file,
+    then loaded twice — the reference's way (each tensor read into a host
+    buffer, src/gguf.cc:621-662, then one host-to-device copy of the AoS
+    blocks, src/cuda_weight_upload.cc; its AoS vector build is left out, in
+    its favour) and through GgufFile.upload (mapped file, device copy,
+    device repack to the tiled layout). GB/s of GGUF bytes, page cache warm
+    for both."""
+    import tempfile
+    import mini_llama_amd.synth as synth
+    import mini_llama_amd.gguf_writer as gw
+    tensors = []
+    for layer in range(layers):
+        for i, (name, n, k) in enumerate(SWEEP_SHAPES):
+            blocks = synth.make_blocks("q4_0", n, k, 7000 + 10 * layer + i)
+            tensors.append((f"blk.{layer}.{name}.weight", [k, n], gw.GGML_Q4_0,
+                            gw.blocks_bytes(blocks)))
+    total = sum(len(t[3]) for t in tensors)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "model.gguf")
+        gw.write_gguf(path, [("general.architecture", gw.STRING, "qwen2")], tensors)
+        del tensors
+        with pkg.GgufFile(path) as g:
+            infos = list(g.tensors)
+            for t in infos:  # warm the page cache
+                g.data(t["name"])
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            ws = [g.upload(t["name"], device="cuda") for t in infos]
+            torch.cuda.synchronize()
+            ours = time.perf_counter() - t0
+        del ws
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        held = []
+        with open(path, "rb") as f:
+            for t in infos:
+                f.seek(t["offset"])
+                raw = np.frombuffer(f.read(t["bytes"]), dtype=np.uint8)
+                held.append(torch.from_numpy(raw.copy()).to("cuda"))
+        torch.cuda.synchronize()
+        ref = time.perf_counter() - t0
+        del held
+        torch.cuda.empty_cache()
+    return {"bytes": total, "tensors": len(infos), "gguf_upload_gbs": total / ours / 1e9,
+            "reference_style_gbs": total / ref / 1e9, "gguf_upload_s": ours,
+            "reference_style_s": ref}
+
+
 def cpu_baseline(qtype, n, k, budget_s=10.0):
     """The reference CPU path (oracle restatement of linearQ40 with the
     reference thread partition), timed on this host's cores."""
@@ -328,6 +378,9 @@ def main():
             sw["frac_hbm"] = round(sw["gbs"] / HBM_PEAK_GBS, 4)
             extra[key] = {kk: (round(v, 3) if isinstance(v, float) else v)
                           for kk, v in sw.items()}
+        gl = bench_gguf_load(pkg, torch)
+        extra["gguf_load"] = {kk: (round(v, 3) if isinstance(v, float) else v)
+                              for kk, v in gl.items()}
         result["configs"] = extra
     if not args.no_cpu:
         log("cpu baseline")

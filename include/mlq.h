@@ -45,6 +45,7 @@ enum mlq_status {
   MLQ_ERR_BUFFER_TOO_SMALL = -4, /* destination/workspace smaller than needed */
   MLQ_ERR_UNSUPPORTED = -5,      /* shape outside what the kernels accept  */
   MLQ_ERR_NO_DEVICE = -6,        /* no usable HIP device                   */
+  MLQ_ERR_FORMAT = -7,           /* malformed GGUF file, see mlq_gguf_last_error */
   MLQ_ERR_HIP = -100             /* HIP runtime error, see mlq_last_hip_error */
 };
 
@@ -176,6 +177,46 @@ int mlq_linear_epi(const mlq_weight* w, const float* x, float* y, int m,
  * reference (it keeps ffn_gate and ffn_up as separate tensors). */
 int mlq_interleave_rows(const void* gate, const void* up, int rows,
                         size_t row_bytes, void* out);
+
+/* ---- GGUF (v3) weight files ------------------------------------------
+ * Replaces the reference's GgufReader::load / readGgufTensorRaw
+ * (include/mini_llama/gguf.h:69-96, src/gguf.cc:398-662) for the Linear
+ * weights: the file is memory-mapped and validated with the same rules
+ * (magic, version 3, entry/string/array limits, unique keys and names,
+ * 1..8 non-zero dims, general.alignment a power of two <= 1 MiB, quantized
+ * element counts a multiple of 32, data inside the file). */
+typedef struct mlq_gguf mlq_gguf;  /* an open, mapped file */
+typedef struct {
+  const char* name;    /* valid while the file is open */
+  uint32_t ggml_type;  /* 0 F32, 1 F16, 2 Q4_0, 3 Q4_1, 8 Q8_0, other ids as stored */
+  uint32_t n_dims;
+  uint64_t dims[8];    /* GGUF order: dims[0] innermost (k of an [n][k] matrix) */
+  uint64_t offset;     /* absolute file offset of the tensor data */
+  uint64_t bytes;      /* data size; 0 for types without a known size */
+} mlq_gguf_tensor;
+
+/* Open and validate; MLQ_ERR_FORMAT with a message in mlq_gguf_last_error
+ * (this thread) when the file is not an acceptable GGUF v3 file. */
+int mlq_gguf_open(const char* path, mlq_gguf** out);
+const char* mlq_gguf_last_error(void);
+void mlq_gguf_close(mlq_gguf* g);
+int mlq_gguf_tensor_count(const mlq_gguf* g, int64_t* count);
+/* Absolute offset of the data section and the alignment in force. */
+int mlq_gguf_data_offset(const mlq_gguf* g, uint64_t* offset, uint64_t* alignment);
+int mlq_gguf_tensor_info(const mlq_gguf* g, int64_t index, mlq_gguf_tensor* out);
+/* Index of a tensor by name (MLQ_ERR_SHAPE and -1 when absent). */
+int mlq_gguf_find(const mlq_gguf* g, const char* name, int64_t* index);
+/* The tensor's bytes inside the mapping (NULL for unsized types). */
+const void* mlq_gguf_data(const mlq_gguf* g, int64_t index);
+/* Upload a 2-D Q8_0 / Q4_0 / Q4_1 tensor (dims [k, n]) into the tiled
+ * weight w (layout of mlq_weight_layout(type, n, k), w->base on the
+ * device): one copy from the mapping into aos_dev (device scratch of at
+ * least the tensor's bytes) and the device repack, stream-ordered. No
+ * host-side block vector is built (the reference loader holds one per
+ * tensor, src/gguf_loader.cc:396-411). MLQ_ERR_UNSUPPORTED for other
+ * types, MLQ_ERR_SHAPE when w does not match the tensor. */
+int mlq_gguf_upload(const mlq_gguf* g, int64_t index, void* aos_dev, size_t aos_bytes,
+                    mlq_weight* w, mlq_stream_t stream);
 
 /* Raw GGUF AoS blocks in device memory: the meaning of the `const void*`
  * weight of cudaQ*LinearDeviceWeight / cudaQ*LinearDeviceInput

@@ -33,7 +33,8 @@ GEMV_MAX_ROWS = 8
 STATUS = {
     0: "ok", -1: "invalid argument", -2: "shape mismatch",
     -3: "block count mismatch", -4: "buffer too small",
-    -5: "unsupported shape", -6: "no HIP device", -100: "HIP runtime error",
+    -5: "unsupported shape", -6: "no HIP device", -7: "malformed GGUF file",
+    -100: "HIP runtime error",
 }
 
 
@@ -62,6 +63,18 @@ class MlqWeight(ctypes.Structure):
     ]
 
 
+class MlqGgufTensor(ctypes.Structure):
+    """mlq_gguf_tensor (include/mlq.h)."""
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("ggml_type", ctypes.c_uint32),
+        ("n_dims", ctypes.c_uint32),
+        ("dims", ctypes.c_uint64 * 8),
+        ("offset", ctypes.c_uint64),
+        ("bytes", ctypes.c_uint64),
+    ]
+
+
 # Every symbol declared in include/mlq.h, with its ctypes signature.
 _P, _I, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 _WP = ctypes.POINTER(MlqWeight)
@@ -81,6 +94,16 @@ SIGNATURES = {
     "mlq_linear_ws": ([_WP, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_linear_epi": ([_WP, _P, _P, _I, _P, _I, _P, _Z, _P], _I),
     "mlq_interleave_rows": ([_P, _P, _I, _Z, _P], _I),
+    "mlq_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(_P)], _I),
+    "mlq_gguf_last_error": ([], ctypes.c_char_p),
+    "mlq_gguf_close": ([_P], None),
+    "mlq_gguf_tensor_count": ([_P, ctypes.POINTER(ctypes.c_int64)], _I),
+    "mlq_gguf_data_offset": ([_P, ctypes.POINTER(ctypes.c_uint64),
+                              ctypes.POINTER(ctypes.c_uint64)], _I),
+    "mlq_gguf_tensor_info": ([_P, ctypes.c_int64, ctypes.POINTER(MlqGgufTensor)], _I),
+    "mlq_gguf_find": ([_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)], _I),
+    "mlq_gguf_data": ([_P, ctypes.c_int64], _P),
+    "mlq_gguf_upload": ([_P, ctypes.c_int64, _P, _Z, _WP, _P], _I),
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
     "mlq_set_gemv_split": ([_I], _I),
     "mlq_set_gemm_split": ([_I], _I),
@@ -217,6 +240,85 @@ def upload_glu(qtype: str, gate_blocks, up_blocks, ffn: int, k: int,
     silu(gate) * up."""
     return upload(qtype, interleave_rows(gate_blocks, up_blocks, ffn),
                   2 * ffn, k, device=device)
+
+
+GGML_TYPES = {0: "f32", 1: "f16", 2: "q4_0", 3: "q4_1", 8: "q8_0"}
+
+
+class GgufFile:
+    """A GGUF v3 file, memory-mapped and validated by mlq_gguf_open.
+
+    `tensors` lists every tensor (name, GGML type, dims in GGUF order —
+    dims[0] innermost —, absolute data offset, bytes); `data(name)` returns
+    a copy of its bytes; `upload(name)` makes a TiledWeight of a 2-D
+    q8_0 / q4_0 / q4_1 tensor straight from the mapping (device copy +
+    device repack, no host block vector)."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        st = lib().mlq_gguf_open(os.fsencode(path), ctypes.byref(h))
+        if st != 0:
+            raise MLQError(st, "mlq_gguf_open: " +
+                           lib().mlq_gguf_last_error().decode(errors="replace"), 0)
+        self._h = h
+        count = ctypes.c_int64()
+        _check(lib().mlq_gguf_tensor_count(h, ctypes.byref(count)), "mlq_gguf_tensor_count")
+        off, align = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib().mlq_gguf_data_offset(h, ctypes.byref(off), ctypes.byref(align)),
+               "mlq_gguf_data_offset")
+        self.data_offset, self.alignment = off.value, align.value
+        self.tensors = []
+        for i in range(count.value):
+            t = MlqGgufTensor()
+            _check(lib().mlq_gguf_tensor_info(h, i, ctypes.byref(t)), "mlq_gguf_tensor_info")
+            self.tensors.append({"name": t.name.decode(), "type": t.ggml_type,
+                                 "dims": [int(t.dims[d]) for d in range(t.n_dims)],
+                                 "offset": int(t.offset), "bytes": int(t.bytes)})
+        self._index = {t["name"]: i for i, t in enumerate(self.tensors)}
+
+    def close(self):
+        if self._h:
+            lib().mlq_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def data(self, name: str) -> np.ndarray:
+        i = self._index[name]
+        n = self.tensors[i]["bytes"]
+        ptr = lib().mlq_gguf_data(self._h, i)
+        if not ptr:
+            return np.empty(0, dtype=np.uint8)
+        return np.ctypeslib.as_array(ctypes.cast(ptr, ctypes.POINTER(ctypes.c_uint8)),
+                                     shape=(n,)).copy()
+
+    def upload(self, name: str, device: str = "cuda", stream=None) -> "TiledWeight":
+        import torch
+        i = self._index[name]
+        t = self.tensors[i]
+        if t["type"] not in (2, 3, 8) or len(t["dims"]) != 2:
+            raise ValueError(f"{name}: not a 2-D q8_0/q4_0/q4_1 tensor")
+        qtype = GGML_TYPES[t["type"]]
+        k, n = t["dims"]
+        layout = weight_layout(qtype, n, k)
+        buf = torch.empty(int(layout.bytes), dtype=torch.uint8, device=device)
+        aos = torch.empty(t["bytes"], dtype=torch.uint8, device=device)
+        layout.base = buf.data_ptr()
+        _check(lib().mlq_gguf_upload(self._h, i, aos.data_ptr(), aos.numel(),
+                                     ctypes.byref(layout), _stream(stream)),
+               "mlq_gguf_upload")
+        torch.cuda.current_stream().synchronize() if stream is None else stream.synchronize()
+        return TiledWeight(qtype, n, k, buf, layout)
 
 
 def upload_aos(blocks: np.ndarray, device: str = "cuda"):

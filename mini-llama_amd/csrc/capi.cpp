@@ -58,6 +58,11 @@ bool uses_gemv(const mlq_weight* w, int m) {
 
 }  // namespace
 
+namespace mlq {
+// MLQ status of a HIP result, recorded for mlq_last_hip_error (gguf.cpp).
+int record_hip(hipError_t e) { return hip_status(e); }
+}  // namespace mlq
+
 extern "C" {
 
 const char* mlq_status_string(int status) {
@@ -69,6 +74,7 @@ const char* mlq_status_string(int status) {
     case MLQ_ERR_BUFFER_TOO_SMALL: return "buffer too small";
     case MLQ_ERR_UNSUPPORTED: return "unsupported shape";
     case MLQ_ERR_NO_DEVICE: return "no HIP device";
+    case MLQ_ERR_FORMAT: return "malformed GGUF file";
     case MLQ_ERR_HIP: return "HIP runtime error";
     default: return "unknown status";
   }

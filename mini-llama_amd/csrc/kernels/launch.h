@@ -23,6 +23,9 @@ struct Epilogue {
   int act = kEpiNone;
 };
 
+// capi.cpp: MLQ status of a HIP result, recorded for mlq_last_hip_error.
+int record_hip(hipError_t e);
+
 // repack.hip
 hipError_t launch_repack(int type, const void* aos, int n, int k,
                          const mlq_weight& w, hipStream_t stream);

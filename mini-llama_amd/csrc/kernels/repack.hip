@@ -21,6 +21,10 @@ struct RepackArgs {
   uint16_t* d;
   uint16_t* m;
   Geometry geo;
+  // alignment gaps between and after the regions ([begin, end) byte
+  // offsets from the weight base): zeroed, like the host repack does
+  uint8_t* base;
+  uint64_t gap[3][2];
 };
 
 // One thread per padded (row, block); padding blocks decode to 0.
@@ -29,7 +33,18 @@ __global__ void repack_kernel(RepackArgs a) {
   const int bpr = a.geo.g * kGroupBlocks;  // padded blocks per row
   const uint64_t total = (uint64_t)a.geo.nt * kTileRows * bpr;
   const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
+  if (idx >= total) {
+    uint64_t g = idx - total;
+    for (int i = 0; i < 3; ++i) {
+      const uint64_t len = a.gap[i][1] - a.gap[i][0];
+      if (g < len) {
+        a.base[a.gap[i][0] + g] = 0;
+        return;
+      }
+      g -= len;
+    }
+    return;
+  }
   const int row = (int)(idx / bpr), b = (int)(idx % bpr);
   const bool real = row < a.geo.n && b < a.geo.nb;
   const int bytes = QT == MLQ_Q8_0 ? 34 : (QT == MLQ_Q4_0 ? 18 : 20);
@@ -89,9 +104,21 @@ hipError_t launch_repack(int type, const void* aos, int n, int k,
   a.d = (uint16_t*)((uint8_t*)w.base + w.d_off);
   a.m = type == MLQ_Q4_1 ? (uint16_t*)((uint8_t*)w.base + w.m_off) : nullptr;
   a.geo = geo;
+  a.base = (uint8_t*)w.base;
+  const uint64_t qbytes = unit_count(geo) * kLanes * quant_bytes_per_lane(type);
+  const uint64_t sbytes = scale_count(geo) * 2;
+  const uint64_t d_end = w.d_off + sbytes;
+  a.gap[0][0] = w.qs_off + qbytes;
+  a.gap[0][1] = w.d_off;
+  a.gap[1][0] = d_end;
+  a.gap[1][1] = type == MLQ_Q4_1 ? w.m_off : w.bytes;
+  a.gap[2][0] = type == MLQ_Q4_1 ? w.m_off + sbytes : w.bytes;
+  a.gap[2][1] = w.bytes;
+  const uint64_t gaps = (a.gap[0][1] - a.gap[0][0]) + (a.gap[1][1] - a.gap[1][0]) +
+                        (a.gap[2][1] - a.gap[2][0]);
   const uint64_t total = (uint64_t)geo.nt * kTileRows * geo.g * kGroupBlocks;
   const unsigned threads = 256;
-  const unsigned blocks = (unsigned)((total + threads - 1) / threads);
+  const unsigned blocks = (unsigned)((total + gaps + threads - 1) / threads);
   switch (type) {
     case MLQ_Q8_0:
       repack_kernel<MLQ_Q8_0><<<blocks, threads, 0, stream>>>(a);

@@ -79,25 +79,24 @@ def test_dequant_bit_exact_config_rows(pkg, oracle, cuda, qtype, n, k):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("n,k", [(16, 128), (45, 300), (100, 4096)])
+@pytest.mark.parametrize("n,k", [(16, 128), (45, 300), (100, 4096), (16, 2080)])
 def test_device_repack_equals_host_repack(pkg, cuda, qtype, n, k):
+    """The device repack writes every byte of the tiled image (alignment
+    gaps zeroed), equal to the host repack's; the destination starts out
+    filled with 0xAB so an unwritten byte shows."""
+    import ctypes
+    torch = _torch()
     blocks = make_blocks(qtype, n, k, seed=n + k)
     host = pkg.upload(qtype, blocks, n, k, device=cuda)
-    dev = pkg.repack_device(qtype, pkg.upload_aos(blocks, device=cuda), n, k)
-    _torch().cuda.synchronize()
-    lay = host.layout
-    h = host.buffer.cpu().numpy()
-    d = dev.buffer.cpu().numpy()
-    # compare quant, scale (and min) regions up to their real lengths (the
-    # alignment gaps between regions are never read)
-    geo_units = ((n + 15) // 16) * (((k + 31) // 32 + 3) // 4)
-    qbytes = geo_units * 64 * (32 if qtype == "q8_0" else 16)
-    sbytes = geo_units * 64 * 2
-    assert np.array_equal(h[:qbytes], d[:qbytes])
-    assert np.array_equal(h[lay.d_off:lay.d_off + sbytes], d[lay.d_off:lay.d_off + sbytes])
-    if qtype == "q4_1":
-        assert np.array_equal(h[lay.m_off:lay.m_off + sbytes],
-                              d[lay.m_off:lay.m_off + sbytes])
+    aos = pkg.upload_aos(blocks, device=cuda)
+    lay = pkg.weight_layout(qtype, n, k)
+    buf = torch.full((int(lay.bytes),), 0xAB, dtype=torch.uint8, device=cuda)
+    st = pkg.lib().mlq_repack_device(pkg.TYPES[qtype], aos.data_ptr(),
+                                     aos.numel() // pkg.BLOCK_BYTES[qtype], n, k,
+                                     buf.data_ptr(), buf.numel(), pkg._stream())
+    assert st == 0
+    torch.cuda.synchronize()
+    assert torch.equal(buf, host.buffer)
 
 
 # --------------------------------------------------------------------------
@@ -361,6 +360,32 @@ def test_fused_swiglu(pkg, oracle, cuda, qtype, m, ffn, k):
     bound = (1.1 * np.abs(uo) + np.abs(_silu64(go))) * atol + 1.1 * atol * atol
     err = np.abs(got - ro)
     assert np.all((err <= bound) | (err <= 2e-3 * np.abs(ro))), err.max()
+
+
+def test_gguf_upload_matches_host_repack(pkg, oracle, cuda, tmp_path):
+    """Tensors uploaded straight from a mapped GGUF file (device copy +
+    device repack) are the same tiled bytes as the host repack of the same
+    blocks, and the Linear on them meets the oracle."""
+    import mini_llama_amd.gguf_writer as gw
+    torch = _torch()
+    specs = [("blk.0.attn_q.weight", "q8_0", 40, 96), ("blk.0.ffn_up.weight", "q4_0", 33, 1024),
+             ("blk.0.ffn_down.weight", "q4_1", 16, 2080)]
+    gtype = {"q8_0": gw.GGML_Q8_0, "q4_0": gw.GGML_Q4_0, "q4_1": gw.GGML_Q4_1}
+    blocks = {name: make_blocks(qt, n, k, seed=n + k) for name, qt, n, k in specs}
+    path = str(tmp_path / "w.gguf")
+    gw.write_gguf(path, [("general.architecture", gw.STRING, "qwen2")],
+                  [(name, [k, n], gtype[qt], gw.blocks_bytes(blocks[name]))
+                   for name, qt, n, k in specs], alignment=64)
+    with pkg.GgufFile(path) as g:
+        for name, qt, n, k in specs:
+            _print_case(test="gguf_upload", tensor=name)
+            tw = g.upload(name, device=cuda)
+            ref = pkg.upload(qt, blocks[name], n, k, device=cuda)
+            assert (tw.qtype, tw.n, tw.k) == (qt, n, k)
+            assert torch.equal(tw.buffer, ref.buffer), name
+            x = make_x(3, k, seed=k)
+            got = pkg.linear(tw, _dev(x, cuda)).cpu().numpy()
+            assert tolerance_ok(got, oracle.linear(x, blocks[name], (n, k), qt), x, k).all()
 
 
 @pytest.mark.parametrize("m", [1, 3, 16])
