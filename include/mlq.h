@@ -255,6 +255,137 @@ int mlq_set_gemm_split(int split);
 int mlq_add_bias(float* y, const float* bias, int m, int n,
                  mlq_stream_t stream);
 
+/* ---------------------------------------------------------------------- */
+/* Decode-step operators (fp32 activations, device pointers)              */
+/* ---------------------------------------------------------------------- */
+/* F32 Linear weights use mlq_weight with type MLQ_F32: base holds W [n][k]
+ * fp32 row-major (mlq_weight_layout(MLQ_F32, n, k) gives bytes = 4nk, every
+ * offset 0). mlq_linear, mlq_linear_ws and mlq_linear_epi then run an fp32
+ * HBM-streaming GEMV (any m, no workspace, same epilogues), replacing the
+ * cuBLAS Sgemm of cudaLinearDeviceInput (src/cuda_matmul.cc:205-241) and the
+ * F32 arm of forwardLinearDevice (src/forward.cc:206-209). The GEMM path
+ * override (MLQ_PATH_MFMA) is MLQ_ERR_UNSUPPORTED for them. */
+
+/* RopeType enumerator order (include/mini_llama/model.h:17-20). */
+enum mlq_rope_type { MLQ_ROPE_NORMAL = 0, MLQ_ROPE_NEOX = 1 };
+
+/* y[r] = x[r] * weight / sqrt(mean(x[r]^2) + eps) for rows r of [rows, dim]
+ * (rmsNorm, src/ops.cc:43-72; cudaRmsNormDeviceWeight,
+ * include/mini_llama/cuda_ops.h:40). eps must be finite and positive
+ * (MLQ_ERR_INVALID_ARG otherwise, as src/cuda_ops.cu:99-101). */
+int mlq_rmsnorm(const float* x, const float* weight, float* y, int rows, int dim,
+                float eps, mlq_stream_t stream);
+/* Elementwise over n floats: a + b (cudaElementwiseAddDeviceInput,
+ * cuda_ops.h:57), a * b (cudaElementwiseMulDeviceInput, :52), silu(x) =
+ * x / (1 + exp(-x)) (cudaSiluDeviceInput, :49), silu(gate) * up in one pass
+ * (forwardSwiGluDevice, src/forward.cc:361-370). */
+int mlq_add(const float* a, const float* b, float* y, int64_t n, mlq_stream_t stream);
+int mlq_mul(const float* a, const float* b, float* y, int64_t n, mlq_stream_t stream);
+int mlq_silu(const float* x, float* y, int64_t n, mlq_stream_t stream);
+int mlq_swiglu(const float* gate, const float* up, float* y, int64_t n, mlq_stream_t stream);
+/* y[dim] = table[token] of an fp32 [vocab, dim] table
+ * (cudaEmbeddingLookupDeviceWeight, cuda_ops.h:71); token outside
+ * [0, vocab) is MLQ_ERR_INVALID_ARG. */
+int mlq_embedding(const float* table, int vocab, int dim, int token, float* y,
+                  mlq_stream_t stream);
+/* In-place RoPE of q [n_heads, head_dim] and k [n_kv_heads, head_dim] at
+ * position pos (rope, src/ops.cc:142-218; cudaRopeDeviceInput,
+ * cuda_ops.h:81): pair i rotates by pos * theta^(-2i/head_dim), pairs
+ * (2i, 2i+1) for MLQ_ROPE_NORMAL, (i, i + head_dim/2) for MLQ_ROPE_NEOX.
+ * head_dim must be positive and even (MLQ_ERR_SHAPE); pos < 0 or theta not
+ * finite and positive is MLQ_ERR_INVALID_ARG. */
+int mlq_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim, int pos,
+             float theta, int rope_type, mlq_stream_t stream);
+
+/* A KV cache: keys and values each [n_layers][max_seq_len][n_kv_heads]
+ * [head_dim] fp32 on the device, the layout of CudaKvCache
+ * (include/mini_llama/cuda_kv_cache.h:28-80, src/cuda_kv_cache.cc). */
+typedef struct mlq_kv_cache {
+  float* keys;
+  float* values;
+  int32_t n_layers, max_seq_len, n_kv_heads, head_dim;
+} mlq_kv_cache;
+/* Bytes of each of the two arrays. */
+int mlq_kv_cache_bytes(int n_layers, int max_seq_len, int n_kv_heads, int head_dim,
+                       size_t* bytes);
+/* Store k and v [n_kv_heads * head_dim] at (layer, pos)
+ * (CudaKvCache::writeDevice, cuda_kv_cache.h:53). */
+int mlq_kv_write(const mlq_kv_cache* c, int layer, int pos, const float* k, const float* v,
+                 mlq_stream_t stream);
+/* Workspace of mlq_attention_decode for any pos of this cache. */
+int mlq_attention_workspace(const mlq_kv_cache* c, int n_heads, size_t* bytes);
+/* out [n_heads, head_dim] = softmax(q . K^T / sqrt(head_dim)) . V over
+ * cache positions 0..pos of `layer`, query head h reading kv head
+ * h / (n_heads / n_kv_heads) (cudaAttentionDecodeDeviceInput,
+ * include/mini_llama/cuda_attention.h:22; src/forward.cc:526-565).
+ * Checks of validateAttentionDeviceInputs; n_heads / n_kv_heads > 16 or
+ * head_dim > 256 is MLQ_ERR_UNSUPPORTED. ws: mlq_attention_workspace bytes
+ * (scratch, no initialisation). */
+int mlq_attention_decode(const mlq_kv_cache* c, int layer, int pos, const float* q,
+                         int n_heads, float* out, void* ws, size_t ws_bytes,
+                         mlq_stream_t stream);
+/* *out (device int32) = index of the first maximum of x[n]; NaN never wins
+ * and x[0] = NaN gives 0 (argMax, src/ops.cc:230-246). */
+int mlq_argmax(const float* x, int64_t n, int32_t* out, mlq_stream_t stream);
+
+/* ---- the decode step: one token through the whole model --------------
+ * Weights as uploaded Linear weights (any of F32 / Q8_0 / Q4_0 / Q4_1 per
+ * projection) and fp32 norms, biases and embedding table, all on the
+ * device. Layer fusions chosen at upload time:
+ *  - wk.base == NULL and wv.base == NULL: wq holds the q|k|v rows
+ *    concatenated ([(n_heads + 2 n_kv_heads) head_dim, dim]) and bq, if
+ *    any, the concatenated bias;
+ *  - w_up.base == NULL: w_gate holds gate and up interleaved by
+ *    mlq_interleave_rows ([2 hidden_dim, dim]) and runs with the SwiGLU
+ *    epilogue. */
+typedef struct mlq_layer {
+  const float* attn_norm;            /* [dim] */
+  mlq_weight wq, wk, wv;             /* see above */
+  const float* bq;                   /* optional biases (Qwen2), NULL if none */
+  const float* bk;
+  const float* bv;
+  mlq_weight wo;                     /* [dim, n_heads head_dim] */
+  const float* ffn_norm;             /* [dim] */
+  mlq_weight w_gate, w_up;           /* [hidden_dim, dim] each, or fused */
+  mlq_weight w_down;                 /* [dim, hidden_dim] */
+} mlq_layer;
+
+/* ModelConfig (include/mini_llama/model.h:22-34) plus the weights of
+ * MiniLlamaModel the forward pass reads. */
+typedef struct mlq_model {
+  int32_t vocab_size, dim, hidden_dim, n_layers, n_heads, n_kv_heads, head_dim,
+      max_seq_len;
+  float rope_theta, rms_norm_eps;
+  int32_t rope_type;                 /* enum mlq_rope_type */
+  const float* token_embedding;      /* [vocab_size, dim] */
+  const float* final_norm;           /* [dim] */
+  mlq_weight lm_head;                /* [vocab_size, dim] */
+  const mlq_layer* layers;           /* HOST array of n_layers */
+} mlq_model;
+
+/* Device workspace bytes of mlq_decode_token (256-byte aligned buffer);
+ * also validates every shape of the model. */
+int mlq_decode_workspace(const mlq_model* m, size_t* bytes);
+
+/* logits [vocab_size] (device) for `token` at position `pos`, writing the
+ * layer's K/V rows at pos into the cache: forwardToken's device branch
+ * (src/forward.cc:763-784, forwardLayerDevice :607-640,
+ * computeLogitsDevice :736-745) as one stream-ordered sequence of launches.
+ * token_dev / pos_dev (device int32, may be NULL) replace token / pos, so a
+ * captured HIP graph of one call serves every step; a device token or
+ * position out of range yields NaN logits instead of a fault. The cache must
+ * match the model (layers, kv heads, head_dim, capacity >= max_seq_len). */
+int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int pos,
+                     const int32_t* token_dev, const int32_t* pos_dev, float* logits,
+                     void* ws, size_t ws_bytes, mlq_stream_t stream);
+
+/* Greedy sampling on the device (argMax, src/ops.cc:230-246, as the
+ * sampler's temperature-0 choice): *token_dev = argmax(logits), then
+ * *pos_dev += 1, so decode steps can follow each other with no host
+ * round trip. */
+int mlq_greedy_next(const float* logits, int vocab, int32_t* token_dev, int32_t* pos_dev,
+                    mlq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

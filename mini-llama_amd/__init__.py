@@ -24,7 +24,9 @@ CPP_TEST_PATH = os.path.join(HERE, "test_hip_quant")
 # enum mlq_type (numeric values follow the reference QuantType order)
 F32, Q8_0, Q4_0, Q4_1 = 0, 1, 2, 3
 TYPES = {"q8_0": Q8_0, "q4_0": Q4_0, "q4_1": Q4_1}
+LINEAR_TYPES = {"f32": F32, **TYPES}
 BLOCK_BYTES = {"q8_0": 34, "q4_0": 18, "q4_1": 20}
+ROPE_NORMAL, ROPE_NEOX = 0, 1
 # enum mlq_path
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
 EPI_NONE, EPI_SWIGLU = 0, 1
@@ -75,9 +77,40 @@ class MlqGgufTensor(ctypes.Structure):
     ]
 
 
+class MlqKvCache(ctypes.Structure):
+    """struct mlq_kv_cache (include/mlq.h)."""
+    _fields_ = [("keys", ctypes.c_void_p), ("values", ctypes.c_void_p),
+                ("n_layers", ctypes.c_int32), ("max_seq_len", ctypes.c_int32),
+                ("n_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32)]
+
+
+class MlqLayer(ctypes.Structure):
+    """struct mlq_layer (include/mlq.h)."""
+    _fields_ = [("attn_norm", ctypes.c_void_p),
+                ("wq", MlqWeight), ("wk", MlqWeight), ("wv", MlqWeight),
+                ("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p), ("bv", ctypes.c_void_p),
+                ("wo", MlqWeight), ("ffn_norm", ctypes.c_void_p),
+                ("w_gate", MlqWeight), ("w_up", MlqWeight), ("w_down", MlqWeight)]
+
+
+class MlqModel(ctypes.Structure):
+    """struct mlq_model (include/mlq.h)."""
+    _fields_ = [("vocab_size", ctypes.c_int32), ("dim", ctypes.c_int32),
+                ("hidden_dim", ctypes.c_int32), ("n_layers", ctypes.c_int32),
+                ("n_heads", ctypes.c_int32), ("n_kv_heads", ctypes.c_int32),
+                ("head_dim", ctypes.c_int32), ("max_seq_len", ctypes.c_int32),
+                ("rope_theta", ctypes.c_float), ("rms_norm_eps", ctypes.c_float),
+                ("rope_type", ctypes.c_int32),
+                ("token_embedding", ctypes.c_void_p), ("final_norm", ctypes.c_void_p),
+                ("lm_head", MlqWeight), ("layers", ctypes.POINTER(MlqLayer))]
+
+
 # Every symbol declared in include/mlq.h, with its ctypes signature.
 _P, _I, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 _WP = ctypes.POINTER(MlqWeight)
+_I64, _F = ctypes.c_int64, ctypes.c_float
+_KVP = ctypes.POINTER(MlqKvCache)
+_MP = ctypes.POINTER(MlqModel)
 SIGNATURES = {
     "mlq_status_string": ([_I], ctypes.c_char_p),
     "mlq_last_hip_error": ([], _I),
@@ -107,6 +140,21 @@ SIGNATURES = {
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
     "mlq_set_gemv_split": ([_I], _I),
     "mlq_set_gemm_split": ([_I], _I),
+    "mlq_rmsnorm": ([_P, _P, _P, _I, _I, _F, _P], _I),
+    "mlq_add": ([_P, _P, _P, _I64, _P], _I),
+    "mlq_mul": ([_P, _P, _P, _I64, _P], _I),
+    "mlq_silu": ([_P, _P, _I64, _P], _I),
+    "mlq_swiglu": ([_P, _P, _P, _I64, _P], _I),
+    "mlq_embedding": ([_P, _I, _I, _I, _P, _P], _I),
+    "mlq_rope": ([_P, _P, _I, _I, _I, _I, _F, _I, _P], _I),
+    "mlq_kv_cache_bytes": ([_I, _I, _I, _I, ctypes.POINTER(_Z)], _I),
+    "mlq_kv_write": ([_KVP, _I, _I, _P, _P, _P], _I),
+    "mlq_attention_workspace": ([_KVP, _I, ctypes.POINTER(_Z)], _I),
+    "mlq_attention_decode": ([_KVP, _I, _I, _P, _I, _P, _P, _Z, _P], _I),
+    "mlq_argmax": ([_P, _I64, _P, _P], _I),
+    "mlq_decode_workspace": ([_MP, ctypes.POINTER(_Z)], _I),
+    "mlq_decode_token": ([_MP, _KVP, _I, _I, _P, _P, _P, _P, _Z, _P], _I),
+    "mlq_greedy_next": ([_P, _I, _P, _P, _P], _I),
 }
 
 _LIB = None
@@ -151,7 +199,7 @@ def device_count() -> int:
 
 def weight_layout(qtype: str, n: int, k: int) -> MlqWeight:
     w = MlqWeight()
-    _check(lib().mlq_weight_layout(TYPES[qtype], n, k, ctypes.byref(w)),
+    _check(lib().mlq_weight_layout(LINEAR_TYPES[qtype], n, k, ctypes.byref(w)),
            "mlq_weight_layout")
     return w
 
@@ -194,6 +242,8 @@ class TiledWeight:
     @property
     def gguf_bytes(self) -> int:
         """Size of the same weight as GGUF blocks (the algorithmic bytes)."""
+        if self.qtype == "f32":
+            return 4 * self.n * self.k
         return self.n * ((self.k + 31) // 32) * BLOCK_BYTES[self.qtype]
 
 
@@ -204,6 +254,17 @@ def upload(qtype: str, blocks: np.ndarray, n: int, k: int,
     image, layout = repack_host(qtype, blocks, n, k)
     buf = torch.from_numpy(image).to(device)
     return TiledWeight(qtype, n, k, buf, layout)
+
+
+def upload_f32(w: np.ndarray, device: str = "cuda") -> TiledWeight:
+    """An fp32 [n, k] Linear weight as is (type MLQ_F32: the mlq_linear
+    family runs the fp32 GEMV on it)."""
+    import torch
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    layout = weight_layout("f32", n, k)
+    buf = torch.from_numpy(w.view(np.uint8).reshape(-1).copy()).to(device)
+    return TiledWeight("f32", n, k, buf, layout)
 
 
 def upload_concat(qtype: str, parts, k: int, device: str = "cuda"):

@@ -37,6 +37,17 @@ int check_weight(int type, size_t block_count, int n, int k) {
   return MLQ_OK;
 }
 
+int check_tiled(const mlq_weight* w);
+
+// A Linear weight: tiled quantized, or plain fp32 rows (type MLQ_F32).
+int check_linear_weight(const mlq_weight* w) {
+  if (w == nullptr || w->base == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (w->type != MLQ_F32) return check_tiled(w);
+  if (w->n <= 0 || w->k <= 0) return MLQ_ERR_SHAPE;
+  if (w->bytes < (uint64_t)w->n * (uint64_t)w->k * sizeof(float)) return MLQ_ERR_INVALID_ARG;
+  return MLQ_OK;
+}
+
 int check_tiled(const mlq_weight* w) {
   if (w == nullptr || w->base == nullptr) return MLQ_ERR_INVALID_ARG;
   if (!quant_type(w->type)) return MLQ_ERR_INVALID_ARG;
@@ -104,8 +115,19 @@ size_t mlq_block_bytes(int type) {
 }
 
 int mlq_weight_layout(int type, int n, int k, mlq_weight* out) {
-  if (out == nullptr || !quant_type(type)) return MLQ_ERR_INVALID_ARG;
+  if (out == nullptr || !(quant_type(type) || type == MLQ_F32)) return MLQ_ERR_INVALID_ARG;
   if (n <= 0 || k <= 0) return MLQ_ERR_SHAPE;
+  if (type == MLQ_F32) {
+    mlq_weight w;
+    std::memset(&w, 0, sizeof w);
+    w.type = type;
+    w.n = n;
+    w.k = k;
+    w.nb = (k + kQK - 1) / kQK;
+    w.bytes = (uint64_t)n * (uint64_t)k * sizeof(float);
+    *out = w;
+    return MLQ_OK;
+  }
   const Geometry geo = geometry(n, k);
   const uint64_t qbytes = unit_count(geo) * kLanes * quant_bytes_per_lane(type);
   const uint64_t sbytes = scale_count(geo) * 2;
@@ -182,10 +204,16 @@ int mlq_dequantize(const mlq_weight* w, int row0, int rows, float* out,
 
 int mlq_linear_path(const mlq_weight* w, const float* x, float* y, int m,
                     int path, mlq_stream_t stream) {
-  int rc = check_tiled(w);
+  int rc = check_linear_weight(w);
   if (rc != MLQ_OK) return rc;
   if (x == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
+  if (w->type == MLQ_F32) {
+    if (path != MLQ_PATH_AUTO && path != MLQ_PATH_GEMV)
+      return path == MLQ_PATH_MFMA ? MLQ_ERR_UNSUPPORTED : MLQ_ERR_INVALID_ARG;
+    return hip_status(
+        launch_linear_f32((const float*)w->base, w->n, w->k, x, y, m, (hipStream_t)stream));
+  }
   const bool gemv_fits = uses_gemv(w, m);
   bool use_gemv;
   switch (path) {
@@ -208,11 +236,11 @@ int mlq_linear(const mlq_weight* w, const float* x, float* y, int m,
 }
 
 int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes) {
-  int rc = check_tiled(w);
+  int rc = check_linear_weight(w);
   if (rc != MLQ_OK) return rc;
   if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
-  *bytes = uses_gemv(w, m)           ? 0
+  *bytes = w->type == MLQ_F32 || uses_gemv(w, m) ? 0
            : m <= kSkinnyMaxRows ? skinny_x_bytes(m, w->k)
                                  : gemm_workspace_bytes(m, w->n, w->k);
   return MLQ_OK;
@@ -221,7 +249,7 @@ int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes) {
 int mlq_linear_epi(const mlq_weight* w, const float* x, float* y, int m,
                    const float* bias, int act, void* workspace,
                    size_t workspace_bytes, mlq_stream_t stream) {
-  int rc = check_tiled(w);
+  int rc = check_linear_weight(w);
   if (rc != MLQ_OK) return rc;
   if (x == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
@@ -231,6 +259,8 @@ int mlq_linear_epi(const mlq_weight* w, const float* x, float* y, int m,
   epi.bias = bias;
   epi.act = act == MLQ_EPI_SWIGLU ? kEpiSwiGLU : kEpiNone;
   const hipStream_t s = (hipStream_t)stream;
+  if (w->type == MLQ_F32)
+    return hip_status(launch_linear_f32((const float*)w->base, w->n, w->k, x, y, m, s, epi));
   if (uses_gemv(w, m)) return hip_status(launch_gemv(*w, x, y, m, s, epi));
   const size_t need = m <= kSkinnyMaxRows ? skinny_x_bytes(m, w->k)
                                            : gemm_workspace_bytes(m, w->n, w->k);

@@ -1,0 +1,368 @@
+// C ABI of the decode-step operators and the whole-token decode step
+// (declarations and contracts in include/mlq.h). Argument checks follow the
+// reference's validators (src/ops.cc:43-72, 187-218; src/cuda_attention.cu
+// validateAttentionDeviceInputs; src/forward.cc:27-58) and report through
+// return codes; every launch is stream-ordered and nothing synchronizes.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "kernels/launch.h"
+#include "mlq.h"
+
+using namespace mlq;
+
+namespace {
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int check_cache(const mlq_kv_cache* c) {
+  if (c == nullptr || c->keys == nullptr || c->values == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (c->n_layers <= 0 || c->max_seq_len <= 0 || c->n_kv_heads <= 0 || c->head_dim <= 0)
+    return MLQ_ERR_SHAPE;
+  return MLQ_OK;
+}
+
+// Attention shape checks of validateAttentionDeviceInputs
+// (src/cuda_attention.cu:84-121) for a given head count.
+int check_heads(const mlq_kv_cache* c, int n_heads) {
+  if (n_heads <= 0) return MLQ_ERR_SHAPE;
+  if (n_heads % c->n_kv_heads != 0) return MLQ_ERR_SHAPE;
+  if (!attention_supported(n_heads, c->n_kv_heads, c->head_dim)) return MLQ_ERR_UNSUPPORTED;
+  return MLQ_OK;
+}
+
+// Every Linear of the model: fused q|k|v when wk.base is null, fused
+// gate|up when w_up.base is null.
+bool qkv_fused(const mlq_layer& l) { return l.wk.base == nullptr && l.wv.base == nullptr; }
+bool glu_fused(const mlq_layer& l) { return l.w_up.base == nullptr; }
+
+struct DecodeBuffers {
+  float* x;     // residual stream [dim]
+  float* x2;    // residual after attention [dim]
+  float* h;     // normalised activations [dim]
+  float* qkv;   // q | k | v
+  float* attn;  // attention output [n_heads * hd]
+  float* ffn;   // silu(gate) * up [hidden]
+  float* gate;  // unfused gate / up outputs [hidden] each
+  float* up;
+  float* apart; // attention partials
+  void* lin;    // Linear workspace
+  size_t lin_bytes;
+  size_t total;
+};
+
+int linear_ws(const mlq_weight& w, size_t* need) {
+  size_t b = 0;
+  const int rc = mlq_linear_workspace(&w, 1, &b);
+  if (rc != MLQ_OK) return rc;
+  if (b > *need) *need = b;
+  return MLQ_OK;
+}
+
+// Shape checks of the model against itself (validateLoadedShapes-like) and the
+// workspace plan; base may be null (sizes only).
+int plan(const mlq_model* m, char* base, DecodeBuffers* b) {
+  if (m == nullptr || m->layers == nullptr || m->token_embedding == nullptr ||
+      m->final_norm == nullptr)
+    return MLQ_ERR_INVALID_ARG;
+  if (m->vocab_size <= 0 || m->dim <= 0 || m->hidden_dim <= 0 || m->n_layers <= 0 ||
+      m->n_heads <= 0 || m->n_kv_heads <= 0 || m->head_dim <= 0 || m->max_seq_len <= 0)
+    return MLQ_ERR_SHAPE;
+  if (m->n_heads % m->n_kv_heads != 0) return MLQ_ERR_SHAPE;
+  if (m->head_dim % 2 != 0) return MLQ_ERR_SHAPE;
+  if (!attention_supported(m->n_heads, m->n_kv_heads, m->head_dim)) return MLQ_ERR_UNSUPPORTED;
+  if (!(std::isfinite(m->rope_theta) && m->rope_theta > 0.0f)) return MLQ_ERR_INVALID_ARG;
+  if (!(std::isfinite(m->rms_norm_eps) && m->rms_norm_eps > 0.0f)) return MLQ_ERR_INVALID_ARG;
+  if (m->rope_type != MLQ_ROPE_NORMAL && m->rope_type != MLQ_ROPE_NEOX) return MLQ_ERR_INVALID_ARG;
+  const int dim = m->dim, hid = m->hidden_dim;
+  const int qd = m->n_heads * m->head_dim, kvd = m->n_kv_heads * m->head_dim;
+  size_t lin = 0;
+  auto expect = [&](const mlq_weight& w, int n, int k) -> int {
+    if (w.base == nullptr) return MLQ_ERR_INVALID_ARG;
+    if (w.n != n || w.k != k) return MLQ_ERR_SHAPE;
+    return linear_ws(w, &lin);
+  };
+  for (int i = 0; i < m->n_layers; ++i) {
+    const mlq_layer& l = m->layers[i];
+    if (l.attn_norm == nullptr || l.ffn_norm == nullptr) return MLQ_ERR_INVALID_ARG;
+    int rc;
+    if (qkv_fused(l)) {
+      if ((rc = expect(l.wq, qd + 2 * kvd, dim)) != MLQ_OK) return rc;
+    } else {
+      if ((rc = expect(l.wq, qd, dim)) != MLQ_OK) return rc;
+      if ((rc = expect(l.wk, kvd, dim)) != MLQ_OK) return rc;
+      if ((rc = expect(l.wv, kvd, dim)) != MLQ_OK) return rc;
+    }
+    if ((rc = expect(l.wo, dim, qd)) != MLQ_OK) return rc;
+    if (glu_fused(l)) {
+      if ((rc = expect(l.w_gate, 2 * hid, dim)) != MLQ_OK) return rc;
+      if (hid % 8 != 0) return MLQ_ERR_SHAPE;
+    } else {
+      if ((rc = expect(l.w_gate, hid, dim)) != MLQ_OK) return rc;
+      if ((rc = expect(l.w_up, hid, dim)) != MLQ_OK) return rc;
+    }
+    if ((rc = expect(l.w_down, dim, hid)) != MLQ_OK) return rc;
+  }
+  int rc = expect(m->lm_head, m->vocab_size, dim);
+  if (rc != MLQ_OK) return rc;
+
+  size_t off = 0;
+  auto take = [&](size_t floats) {
+    float* p = base ? (float*)(base + off) : nullptr;
+    off += align256(floats * sizeof(float));
+    return p;
+  };
+  b->x = take(dim);
+  b->x2 = take(dim);
+  b->h = take(dim);
+  b->qkv = take((size_t)qd + 2 * kvd);
+  b->attn = take(qd);
+  b->ffn = take(hid);
+  b->gate = take(hid);
+  b->up = take(hid);
+  b->apart = (float*)(base ? base + off : nullptr);
+  off += align256(attention_workspace_bytes(m->n_heads, m->head_dim, m->max_seq_len));
+  b->lin = base ? base + off : nullptr;
+  b->lin_bytes = lin;
+  off += align256(lin);
+  b->total = off;
+  return MLQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mlq_rmsnorm(const float* x, const float* weight, float* y, int rows, int dim, float eps,
+                mlq_stream_t stream) {
+  if (x == nullptr || weight == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (rows <= 0 || dim <= 0) return MLQ_ERR_SHAPE;
+  // cudaRmsNormDeviceWeight (src/cuda_ops.cu:99-101)
+  if (!(std::isfinite(eps) && eps > 0.0f)) return MLQ_ERR_INVALID_ARG;
+  return record_hip(launch_rmsnorm(x, weight, y, rows, dim, eps, (hipStream_t)stream));
+}
+
+static int eltwise(int op, const float* a, const float* b, float* y, int64_t n,
+                   mlq_stream_t stream) {
+  if (a == nullptr || y == nullptr || (op != kEltSilu && b == nullptr)) return MLQ_ERR_INVALID_ARG;
+  if (n <= 0) return MLQ_ERR_SHAPE;
+  return record_hip(launch_eltwise(op, a, b, y, n, (hipStream_t)stream));
+}
+
+int mlq_add(const float* a, const float* b, float* y, int64_t n, mlq_stream_t stream) {
+  return eltwise(kEltAdd, a, b, y, n, stream);
+}
+int mlq_mul(const float* a, const float* b, float* y, int64_t n, mlq_stream_t stream) {
+  return eltwise(kEltMul, a, b, y, n, stream);
+}
+int mlq_silu(const float* x, float* y, int64_t n, mlq_stream_t stream) {
+  return eltwise(kEltSilu, x, nullptr, y, n, stream);
+}
+int mlq_swiglu(const float* gate, const float* up, float* y, int64_t n, mlq_stream_t stream) {
+  return eltwise(kEltSwiGLU, gate, up, y, n, stream);
+}
+
+int mlq_embedding(const float* table, int vocab, int dim, int token, float* y,
+                  mlq_stream_t stream) {
+  if (table == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (vocab <= 0 || dim <= 0) return MLQ_ERR_SHAPE;
+  if (token < 0 || token >= vocab) return MLQ_ERR_INVALID_ARG;
+  return record_hip(launch_embedding(table, vocab, dim, nullptr, token, y, (hipStream_t)stream));
+}
+
+int mlq_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim, int pos,
+             float theta, int rope_type, mlq_stream_t stream) {
+  if (q == nullptr || k == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0)
+    return MLQ_ERR_SHAPE;
+  if (pos < 0 || !(std::isfinite(theta) && theta > 0.0f)) return MLQ_ERR_INVALID_ARG;
+  if (rope_type != MLQ_ROPE_NORMAL && rope_type != MLQ_ROPE_NEOX) return MLQ_ERR_INVALID_ARG;
+  RopeLaunch r;
+  r.q = q;
+  r.k = k;
+  r.n_heads = n_heads;
+  r.n_kv = n_kv_heads;
+  r.hd = head_dim;
+  r.neox = rope_type == MLQ_ROPE_NEOX;
+  r.pos = pos;
+  r.theta = theta;
+  return record_hip(launch_rope(r, (hipStream_t)stream));
+}
+
+int mlq_kv_cache_bytes(int n_layers, int max_seq_len, int n_kv_heads, int head_dim,
+                       size_t* bytes) {
+  if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (n_layers <= 0 || max_seq_len <= 0 || n_kv_heads <= 0 || head_dim <= 0)
+    return MLQ_ERR_SHAPE;
+  *bytes = (size_t)n_layers * max_seq_len * n_kv_heads * head_dim * sizeof(float);
+  return MLQ_OK;
+}
+
+int mlq_kv_write(const mlq_kv_cache* c, int layer, int pos, const float* k, const float* v,
+                 mlq_stream_t stream) {
+  int rc = check_cache(c);
+  if (rc != MLQ_OK) return rc;
+  if (k == nullptr || v == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (layer < 0 || layer >= c->n_layers || pos < 0 || pos >= c->max_seq_len)
+    return MLQ_ERR_SHAPE;
+  const int n = c->n_kv_heads * c->head_dim;
+  const size_t row = ((size_t)layer * c->max_seq_len + pos) * n;
+  return record_hip(launch_kv_write(c->keys, c->values, k, v, row, n, (hipStream_t)stream));
+}
+
+int mlq_attention_workspace(const mlq_kv_cache* c, int n_heads, size_t* bytes) {
+  int rc = check_cache(c);
+  if (rc != MLQ_OK) return rc;
+  if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
+  if ((rc = check_heads(c, n_heads)) != MLQ_OK) return rc;
+  *bytes = attention_workspace_bytes(n_heads, c->head_dim, c->max_seq_len);
+  return MLQ_OK;
+}
+
+int mlq_attention_decode(const mlq_kv_cache* c, int layer, int pos, const float* q,
+                         int n_heads, float* out, void* ws, size_t ws_bytes,
+                         mlq_stream_t stream) {
+  int rc = check_cache(c);
+  if (rc != MLQ_OK) return rc;
+  if (q == nullptr || out == nullptr || ws == nullptr) return MLQ_ERR_INVALID_ARG;
+  if ((rc = check_heads(c, n_heads)) != MLQ_OK) return rc;
+  if (layer < 0 || layer >= c->n_layers || pos < 0 || pos >= c->max_seq_len)
+    return MLQ_ERR_SHAPE;
+  if (ws_bytes < attention_workspace_bytes(n_heads, c->head_dim, pos + 1))
+    return MLQ_ERR_BUFFER_TOO_SMALL;
+  AttnLaunch a;
+  a.q = q;
+  a.keys = c->keys;
+  a.values = c->values;
+  a.out = out;
+  a.ws = (float*)ws;
+  a.layer = layer;
+  a.max_seq = c->max_seq_len;
+  a.n_heads = n_heads;
+  a.n_kv = c->n_kv_heads;
+  a.hd = c->head_dim;
+  a.max_len = pos + 1;
+  a.pos = pos;
+  return record_hip(launch_attention(a, (hipStream_t)stream));
+}
+
+int mlq_argmax(const float* x, int64_t n, int32_t* out, mlq_stream_t stream) {
+  if (x == nullptr || out == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (n <= 0) return MLQ_ERR_SHAPE;
+  return record_hip(launch_argmax(x, n, out, nullptr, (hipStream_t)stream));
+}
+
+int mlq_greedy_next(const float* logits, int vocab, int32_t* token_dev, int32_t* pos_dev,
+                    mlq_stream_t stream) {
+  if (logits == nullptr || token_dev == nullptr || pos_dev == nullptr)
+    return MLQ_ERR_INVALID_ARG;
+  if (vocab <= 0) return MLQ_ERR_SHAPE;
+  return record_hip(launch_argmax(logits, vocab, token_dev, pos_dev, (hipStream_t)stream));
+}
+
+int mlq_decode_workspace(const mlq_model* m, size_t* bytes) {
+  if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
+  DecodeBuffers b;
+  const int rc = plan(m, nullptr, &b);
+  if (rc != MLQ_OK) return rc;
+  *bytes = b.total;
+  return MLQ_OK;
+}
+
+int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int pos,
+                     const int32_t* token_dev, const int32_t* pos_dev, float* logits,
+                     void* ws, size_t ws_bytes, mlq_stream_t stream) {
+  DecodeBuffers b;
+  int rc = plan(m, (char*)ws, &b);
+  if (rc != MLQ_OK) return rc;
+  if ((rc = check_cache(c)) != MLQ_OK) return rc;
+  if (logits == nullptr || ws == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (((uintptr_t)ws & 255u) != 0) return MLQ_ERR_INVALID_ARG;
+  if (ws_bytes < b.total) return MLQ_ERR_BUFFER_TOO_SMALL;
+  if (c->n_layers != m->n_layers || c->n_kv_heads != m->n_kv_heads ||
+      c->head_dim != m->head_dim || c->max_seq_len < m->max_seq_len)
+    return MLQ_ERR_SHAPE;
+  // validateForwardInputs (src/forward.cc:27-58) for host-side scalars
+  if (token_dev == nullptr && (token < 0 || token >= m->vocab_size)) return MLQ_ERR_INVALID_ARG;
+  if (pos_dev == nullptr && (pos < 0 || pos >= m->max_seq_len)) return MLQ_ERR_INVALID_ARG;
+
+  const hipStream_t s = (hipStream_t)stream;
+  const int dim = m->dim, hd = m->head_dim;
+  const int qd = m->n_heads * hd, kvd = m->n_kv_heads * hd;
+  auto linear = [&](const mlq_weight& w, const float* x, float* y, const float* bias,
+                    int act) {
+    return mlq_linear_epi(&w, x, y, 1, bias, act, b.lin, b.lin_bytes, stream);
+  };
+  auto hip = [](hipError_t e) { return record_hip(e); };
+
+  if ((rc = hip(launch_embedding(m->token_embedding, m->vocab_size, dim, token_dev, token,
+                                 b.x, s))) != MLQ_OK)
+    return rc;
+  for (int li = 0; li < m->n_layers; ++li) {
+    const mlq_layer& l = m->layers[li];
+    // attention sublayer (forwardLayerDevice, src/forward.cc:607-640)
+    if ((rc = hip(launch_rmsnorm(b.x, l.attn_norm, b.h, 1, dim, m->rms_norm_eps, s))) != MLQ_OK)
+      return rc;
+    if (qkv_fused(l)) {
+      if ((rc = linear(l.wq, b.h, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+    } else {
+      if ((rc = linear(l.wq, b.h, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = linear(l.wk, b.h, b.qkv + qd, l.bk, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = linear(l.wv, b.h, b.qkv + qd + kvd, l.bv, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+    }
+    RopeLaunch r;
+    r.q = b.qkv;
+    r.k = b.qkv + qd;
+    r.v = b.qkv + qd + kvd;
+    r.keys = c->keys;
+    r.values = c->values;
+    r.n_heads = m->n_heads;
+    r.n_kv = m->n_kv_heads;
+    r.hd = hd;
+    r.neox = m->rope_type == MLQ_ROPE_NEOX;
+    r.layer = li;
+    r.max_seq = c->max_seq_len;
+    r.pos_dev = pos_dev;
+    r.pos = pos;
+    r.theta = m->rope_theta;
+    if ((rc = hip(launch_rope(r, s))) != MLQ_OK) return rc;
+    AttnLaunch a;
+    a.q = b.qkv;
+    a.keys = c->keys;
+    a.values = c->values;
+    a.out = b.attn;
+    a.ws = b.apart;
+    a.layer = li;
+    a.max_seq = c->max_seq_len;
+    a.n_heads = m->n_heads;
+    a.n_kv = m->n_kv_heads;
+    a.hd = hd;
+    a.max_len = pos_dev != nullptr ? m->max_seq_len : pos + 1;
+    a.pos_dev = pos_dev;
+    a.pos = pos;
+    if ((rc = hip(launch_attention(a, s))) != MLQ_OK) return rc;
+    // x2 = x + wo . attn: the residual enters as the projection's bias
+    if ((rc = linear(l.wo, b.attn, b.x2, b.x, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+    // FFN sublayer
+    if ((rc = hip(launch_rmsnorm(b.x2, l.ffn_norm, b.h, 1, dim, m->rms_norm_eps, s))) != MLQ_OK)
+      return rc;
+    if (glu_fused(l)) {
+      if ((rc = linear(l.w_gate, b.h, b.ffn, nullptr, MLQ_EPI_SWIGLU)) != MLQ_OK) return rc;
+    } else {
+      if ((rc = linear(l.w_gate, b.h, b.gate, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = linear(l.w_up, b.h, b.up, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = hip(launch_eltwise(kEltSwiGLU, b.gate, b.up, b.ffn, m->hidden_dim, s))) != MLQ_OK)
+        return rc;
+    }
+    // x = x2 + w_down . ffn
+    if ((rc = linear(l.w_down, b.ffn, b.x, b.x2, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+  }
+  // computeLogitsDevice (src/forward.cc:736-745)
+  if ((rc = hip(launch_rmsnorm(b.x, m->final_norm, b.h, 1, dim, m->rms_norm_eps, s))) != MLQ_OK)
+    return rc;
+  return linear(m->lm_head, b.h, logits, nullptr, MLQ_EPI_NONE);
+}
+
+}  // extern "C"

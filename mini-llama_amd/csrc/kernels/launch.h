@@ -73,4 +73,57 @@ hipError_t launch_x_to_frag(const float* x, _Float16* xf, int m, int k,
 hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int m,
                          hipStream_t stream, const Epilogue& epi = Epilogue());
 
+// linear_f32.hip: fp32 W [n][k], any m (passes of up to 8 rows).
+hipError_t launch_linear_f32(const float* w, int n, int k, const float* x, float* y, int m,
+                             hipStream_t stream, const Epilogue& epi = Epilogue());
+
+// decode_ops.hip: the decode-step operators.
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim,
+                          float eps, hipStream_t stream);
+enum { kEltAdd = 0, kEltMul = 1, kEltSilu = 2, kEltSwiGLU = 3 };
+hipError_t launch_eltwise(int op, const float* a, const float* b, float* y, int64_t n,
+                          hipStream_t stream);
+// token_dev (device int32, may be null) overrides token.
+hipError_t launch_embedding(const float* table, int vocab, int dim, const int32_t* token_dev,
+                            int token, float* y, hipStream_t stream);
+// RoPE on q [n_heads][hd] and k [n_kv][hd] at position pos (pos_dev
+// overrides). With keys/values non-null the rotated k and v go to cache row
+// (layer, pos) of a [layers][max_seq][n_kv][hd] cache and k is left as is.
+struct RopeLaunch {
+  float* q = nullptr;
+  float* k = nullptr;
+  const float* v = nullptr;
+  float* keys = nullptr;
+  float* values = nullptr;
+  int n_heads = 0, n_kv = 0, hd = 0, neox = 0;
+  int layer = 0, max_seq = 0;
+  const int32_t* pos_dev = nullptr;
+  int pos = 0;
+  float theta = 10000.0f;
+};
+hipError_t launch_rope(const RopeLaunch& r, hipStream_t stream);
+hipError_t launch_kv_write(float* keys, float* values, const float* k, const float* v,
+                           size_t row, int n, hipStream_t stream);
+// Decode attention of q [n_heads][hd] over cache positions 0..pos of `layer`.
+// max_len bounds pos + 1 (grid and workspace size); ws holds
+// attention_workspace_bytes(n_heads, hd, max_len) bytes.
+struct AttnLaunch {
+  const float* q = nullptr;
+  const float* keys = nullptr;
+  const float* values = nullptr;
+  float* out = nullptr;
+  float* ws = nullptr;
+  int layer = 0, max_seq = 0, n_heads = 0, n_kv = 0, hd = 0;
+  int max_len = 0;
+  const int32_t* pos_dev = nullptr;
+  int pos = 0;
+};
+bool attention_supported(int n_heads, int n_kv, int hd);
+int attention_chunks(int hd, int max_len);
+size_t attention_workspace_bytes(int n_heads, int hd, int max_len);
+hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream);
+// out = argmax(x) (first maximum, NaN never wins); pos_dev += 1 when non-null.
+hipError_t launch_argmax(const float* x, int64_t n, int32_t* out, int32_t* pos_dev,
+                         hipStream_t stream);
+
 }  // namespace mlq

@@ -45,3 +45,74 @@ def make_blocks(qtype: str, n: int, k: int, seed: int) -> np.ndarray:
 def make_x(m: int, k: int, seed: int) -> np.ndarray:
     rng = np.random.default_rng(seed)
     return rng.standard_normal((m, k), dtype=np.float32)
+
+
+# ---- synthetic decoder models ---------------------------------------------------
+# Element RMS of each code distribution (q8_0: U{-127..127}; q4_0: nibble - 8;
+# q4_1: nibble - 7.5 with m = -7.5 d): the scale d is drawn as |N(0, s)| with
+# s = rms / code_rms so a weight row has the requested element RMS.
+_CODE_RMS = {"q8_0": float(np.sqrt(127 * 128 / 3)), "q4_0": float(np.sqrt(21.5)),
+             "q4_1": float(np.sqrt(21.25))}
+
+
+def make_blocks_scaled(qtype: str, n: int, k: int, seed: int, rms: float) -> np.ndarray:
+    """GGUF blocks whose dequantized elements have RMS ~ rms (zero mean)."""
+    rng = np.random.default_rng(seed)
+    count = n * ((k + 31) // 32)
+    out = np.empty(count, BLOCK_DTYPES[qtype])
+    d = np.abs(rng.normal(0.0, rms / _CODE_RMS[qtype], count))
+    if qtype == "q8_0":
+        out["qs"] = rng.integers(-127, 128, (count, 32), dtype=np.int8)
+    else:
+        out["qs"] = rng.integers(0, 256, (count, 16), dtype=np.uint8)
+    if qtype == "q4_1":
+        out["m"] = f16_bits(-7.5 * d)
+    out["d"] = f16_bits(d)
+    return out
+
+
+def _linear(qtype: str, n: int, k: int, seed: int) -> dict:
+    rms = 1.0 / np.sqrt(k)
+    if qtype == "f32":
+        rng = np.random.default_rng(seed)
+        return {"type": "f32", "shape": (n, k),
+                "data": (rng.standard_normal((n, k)) * rms).astype(np.float32)}
+    return {"type": qtype, "shape": (n, k), "data": make_blocks_scaled(qtype, n, k, seed, rms)}
+
+
+def synthetic_model(config: dict, qtype: str = "q4_0", seed: int = 0,
+                    bias: bool = False, lm_head_type: str | None = None) -> dict:
+    """A random decoder in the model-dict format of mini_llama_amd.decode:
+    every projection of type `qtype` with element RMS 1/sqrt(in_features),
+    norm weights 1 + N(0, 0.1), embedding N(0, 1), optional q/k/v biases
+    N(0, 0.1) (Qwen2 style). `config` holds the ModelConfig fields."""
+    c = dict(config)
+    c.setdefault("head_dim", c["dim"] // c["n_heads"])
+    c.setdefault("rope_theta", 10000.0)
+    c.setdefault("rms_norm_eps", 1e-5)
+    c.setdefault("rope_type", 0)
+    rng = np.random.default_rng(seed)
+    dim, hid, hd = c["dim"], c["hidden_dim"], c["head_dim"]
+    qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
+
+    def norm():
+        return (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+
+    layers = []
+    for li in range(c["n_layers"]):
+        s = seed * 1000 + li * 16
+        layer = {"attention_norm": norm(),
+                 "wq": _linear(qtype, qd, dim, s + 1), "wk": _linear(qtype, kvd, dim, s + 2),
+                 "wv": _linear(qtype, kvd, dim, s + 3), "wo": _linear(qtype, dim, qd, s + 4),
+                 "ffn_norm": norm(),
+                 "w_gate": _linear(qtype, hid, dim, s + 5), "w_up": _linear(qtype, hid, dim, s + 6),
+                 "w_down": _linear(qtype, dim, hid, s + 7)}
+        if bias:
+            for name, n in (("bq", qd), ("bk", kvd), ("bv", kvd)):
+                layer[name] = (0.1 * rng.standard_normal(n)).astype(np.float32)
+        layers.append(layer)
+    return {"config": c,
+            "token_embedding": rng.standard_normal((c["vocab_size"], dim)).astype(np.float32),
+            "final_norm": norm(),
+            "lm_head": _linear(lm_head_type or qtype, c["vocab_size"], dim, seed * 1000 + 999),
+            "layers": layers}

@@ -160,3 +160,159 @@ def linear_raw(x: np.ndarray, blocks: np.ndarray, n: int, k_w: int,
     return getattr(_lib(flavor), f"ref_linear_{qtype}")(
         _ptr(x), rows, k, _ptr(blocks), blocks.size, n, k_w, _ptr(y),
         int(threads))
+
+
+# ---- decode-step operators and the forward pass (forward_ref.c) ----------------
+_FWD_READY: set = set()
+
+
+def _fwd(flavor: str = "scalar") -> ctypes.CDLL:
+    lib = _lib(flavor)
+    if flavor in _FWD_READY:
+        return lib
+    P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    lib.ref_rmsnorm.argtypes = [P, P, P, I, F]
+    lib.ref_rmsnorm.restype = None
+    lib.ref_softmax.argtypes = [P, P, I]
+    lib.ref_softmax.restype = I
+    lib.ref_silu.argtypes = [P, P, I]
+    lib.ref_silu.restype = None
+    lib.ref_swiglu.argtypes = [P, P, P, I]
+    lib.ref_swiglu.restype = None
+    lib.ref_rope.argtypes = [P, P, I, I, I, I, F, I]
+    lib.ref_rope.restype = I
+    lib.ref_attention.argtypes = [P, P, P, I, I, I, I, I, I, P]
+    lib.ref_attention.restype = None
+    lib.ref_linear_f32.argtypes = [P, P, P, I, I]
+    lib.ref_linear_f32.restype = None
+    lib.ref_argmax.argtypes = [P, I]
+    lib.ref_argmax.restype = I
+    _FWD_READY.add(flavor)
+    return lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    """rmsNorm (ops.cc:43-72) on one vector."""
+    x, w = _f32(x), _f32(w)
+    y = np.empty_like(x)
+    _fwd().ref_rmsnorm(_ptr(x), _ptr(w), _ptr(y), x.size, eps)
+    return y
+
+
+def softmax(x) -> np.ndarray:
+    """softmax (ops.cc:74-109)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    if _fwd().ref_softmax(_ptr(x), _ptr(y), x.size) != 0:
+        raise ValueError("softmax: empty input")
+    return y
+
+
+def silu(x) -> np.ndarray:
+    """silu (ops.cc:111-119)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    _fwd().ref_silu(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def swiglu(gate, up) -> np.ndarray:
+    """swiGlu (ops.cc:137-140)."""
+    g, u = _f32(gate), _f32(up)
+    if g.shape != u.shape:
+        raise ValueError("swiglu: shape mismatch")
+    y = np.empty_like(g)
+    _fwd().ref_swiglu(_ptr(g), _ptr(u), _ptr(y), g.size)
+    return y
+
+
+def rope(q, k, pos: int, theta: float, rope_type: int = 0):
+    """rope (ops.cc:142-228) on copies of q [n_heads, hd] and k [n_kv, hd]."""
+    q, k = _f32(q).copy(), _f32(k).copy()
+    if q.ndim != 2 or k.ndim != 2 or q.shape[1] != k.shape[1]:
+        raise ValueError("rope: expected q [n_heads, hd] and k [n_kv, hd]")
+    rc = _fwd().ref_rope(_ptr(q), _ptr(k), q.shape[0], k.shape[0], q.shape[1], int(pos),
+                         float(theta), int(rope_type))
+    if rc != 0:
+        raise ValueError("rope: rejected arguments")
+    return q, k
+
+
+def attention(q, keys, values, layer: int, pos: int) -> np.ndarray:
+    """forwardAttention's CPU arithmetic (forward.cc:526-565): q [n_heads, hd]
+    against cache rows 0..pos of `layer` (cache [layers, max_seq, n_kv, hd])."""
+    q, keys, values = _f32(q), _f32(keys), _f32(values)
+    n_layers, max_seq, n_kv, hd = keys.shape
+    out = np.empty_like(q)
+    _fwd().ref_attention(_ptr(q), _ptr(keys), _ptr(values), int(layer), int(pos),
+                         q.shape[0], n_kv, hd, max_seq, _ptr(out))
+    return out
+
+
+def linear_f32(x, w) -> np.ndarray:
+    """linearNaive (matmul_dispatch.cc:32-50): x [K] times W [N, K]^T."""
+    x, w = _f32(x).reshape(-1), _f32(w)
+    y = np.empty(w.shape[0], np.float32)
+    _fwd().ref_linear_f32(_ptr(x), _ptr(w), _ptr(y), w.shape[0], w.shape[1])
+    return y
+
+
+def argmax(x) -> int:
+    """argMax (ops.cc:230-246)."""
+    x = _f32(x).reshape(-1)
+    return int(_fwd().ref_argmax(_ptr(x), x.size))
+
+
+def linear_weight(x, w: dict) -> np.ndarray:
+    """The Linear dispatch of forwardLinear's CPU branch (ops.cc:28-40) for a
+    model-dict weight {"type", "shape", "data"}."""
+    if w["type"] == "f32":
+        return linear_f32(x, np.asarray(w["data"], np.float32).reshape(w["shape"]))
+    return linear(_f32(x).reshape(-1), w["data"], w["shape"], w["type"])
+
+
+def new_cache(model: dict):
+    """Zeroed K and V caches [layers, max_seq, n_kv, hd] (KvCache)."""
+    c = model["config"]
+    hd = c.get("head_dim", c["dim"] // c["n_heads"])
+    shape = (c["n_layers"], c["max_seq_len"], c["n_kv_heads"], hd)
+    return np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+
+
+def forward_token(model: dict, cache, token: int, pos: int) -> np.ndarray:
+    """forwardToken's CPU branch (forward.cc:763-797): embedding, every
+    forwardLayer (:642-730) and computelogits (:747-761). `cache` is the
+    (keys, values) pair from new_cache, updated at `pos` in place."""
+    c = model["config"]
+    keys, values = cache
+    nh, nkv = c["n_heads"], c["n_kv_heads"]
+    hd = c.get("head_dim", c["dim"] // nh)
+    eps = c["rms_norm_eps"]
+    if not (0 <= token < c["vocab_size"]) or not (0 <= pos < c["max_seq_len"]):
+        raise ValueError("forward_token: token or position out of range")
+    x = _f32(model["token_embedding"][token])
+    for li, lw in enumerate(model["layers"]):
+        h = rmsnorm(x, lw["attention_norm"], eps)
+        parts = []
+        for wname, bname in (("wq", "bq"), ("wk", "bk"), ("wv", "bv")):
+            y = linear_weight(h, lw[wname])
+            b = lw.get(bname)
+            if b is not None and np.size(b):
+                y = (y + _f32(b)).astype(np.float32)  # addOptionalBias (:402-416)
+            parts.append(y)
+        q, k = rope(parts[0].reshape(nh, hd), parts[1].reshape(nkv, hd), pos,
+                    c["rope_theta"], c.get("rope_type", 0))
+        keys[li, pos] = k
+        values[li, pos] = parts[2].reshape(nkv, hd)
+        att = attention(q, keys, values, li, pos)
+        proj = linear_weight(att.reshape(-1), lw["wo"])
+        x = (x + proj).astype(np.float32)  # forwardAdd (:312-330)
+        h = rmsnorm(x, lw["ffn_norm"], eps)
+        ff = linear_weight(swiglu(linear_weight(h, lw["w_gate"]), linear_weight(h, lw["w_up"])),
+                           lw["w_down"])
+        x = (x + ff).astype(np.float32)
+    return linear_weight(rmsnorm(x, model["final_norm"], eps), model["lm_head"])
