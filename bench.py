@@ -13,6 +13,10 @@ Also reported in the same line: the q8_0 prefill GEMM (configs[4], M=512,
 W [11008, 4096]) in TFLOP/s against the dense fp16 MFMA peak, and the
 reference CPU path (the oracle restatement) timed on the host cores.
 `--all` adds every BASELINE configuration and the 196-GEMV decode sweep.
+`decode_step` reports whole-model decode: a Qwen2-7B-shaped q4_0
+model stepped token by token through mlq_decode_token, captured with its
+greedy sampling as one HIP graph, in tokens/s and algorithmic GB/s (weights
++ KV cache rows read per token).
 
 Profiling modes (one kernel family per run, for rocprofv3 counter passes):
 `--mode headline` launches only the headline GEMV (eagerly with `--eager`),
@@ -264,6 +268,74 @@ def bench_gguf_load(pkg, torch, layers=4):
             "reference_style_s": ref}
 
 
+QWEN2_7B = dict(vocab_size=152064, dim=3584, hidden_dim=18944, n_layers=28, n_heads=28,
+                n_kv_heads=4, max_seq_len=4096, rope_theta=1e6, rms_norm_eps=1e-6,
+                rope_type=1)
+
+
+def decode_bytes(dm, pos):
+    """Algorithmic HBM bytes of one decode step at position `pos`: every
+    Linear weight once (GGUF bytes), the KV rows 0..pos of every layer read
+    and one row written, the embedding row and the logits."""
+    c = dm.config
+    row = c["n_kv_heads"] * c["head_dim"] * 4
+    kv = c["n_layers"] * (2 * (pos + 1) * row + 2 * row)
+    return dm.weight_bytes + kv + 4 * c["dim"] + 4 * c["vocab_size"]
+
+
+def bench_decode(pkg, torch, steps, warmup, context=1024, qtype="q4_0"):
+    """Whole decode steps of a Qwen2-7B-shaped q4_0 model (28 layers, q|k|v
+    biases, NeoX rope, random weights) at positions context..context+steps-1:
+    eager mlq_decode_token calls, then one HIP graph of step + greedy
+    sampling replayed per token. Tokens/s and algorithmic GB/s."""
+    import mini_llama_amd.decode as dec
+    import mini_llama_amd.synth as synth
+    log(f"decode: building a {QWEN2_7B['n_layers']}-layer {qtype} model on the device")
+    model = synth.synthetic_model_device(QWEN2_7B, qtype, seed=7, bias=True)
+    dm = dec.DecodeModel(model)
+    del model
+    torch.cuda.synchronize()
+    n_eager = max(5, min(steps, 50))
+    for i in range(max(warmup, 1)):
+        dm.forward_token(1, context + i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(n_eager):
+        dm.forward_token(1 + i, context + i)
+    end.record()
+    torch.cuda.synchronize()
+    eager_ms = start.elapsed_time(end) / n_eager
+    log("decode: capturing the step graph")
+    dm.token_dev.fill_(1)
+    dm.pos_dev.fill_(context)
+    g = dm.greedy_graph()
+    for _ in range(max(warmup, 1)):
+        g.replay()
+    dm.pos_dev.fill_(context)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    graph_ms = start.elapsed_time(end) / steps
+    end_pos = int(dm.pos_dev.item())
+    assert end_pos == context + steps, end_pos
+    assert np.isfinite(dm.logits.cpu().numpy()).all()
+    nbytes = decode_bytes(dm, context + steps // 2)
+    gbs = nbytes / (graph_ms * 1e-3) / 1e9
+    return {"workload": f"Qwen2-7B-shaped {qtype} decode step (28 layers, dim 3584, FFN 18944, "
+                        "28/4 heads, head_dim 128, vocab 152064, q|k|v bias), "
+                        f"positions {context}..{context + steps - 1}",
+            "tokens_per_s": 1e3 / graph_ms, "ms_per_token": graph_ms,
+            "ms_per_token_eager": eager_ms, "bytes_per_token": nbytes,
+            "weight_bytes": dm.weight_bytes, "gbs": gbs, "steps": steps,
+            "roofline_tokens_per_s": HBM_PEAK_GBS * 1e9 / nbytes,
+            "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
 def cpu_baseline(qtype, n, k, budget_s=10.0):
     """The reference CPU path (oracle restatement of linearQ40 with the
     reference thread partition), timed on this host's cores."""
@@ -298,8 +370,10 @@ def main():
                     help="also run every BASELINE config and the decode sweep")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--mode", choices=["full", "headline", "copy"],
-                    default="full", help="headline/copy: profiling runs")
+    ap.add_argument("--mode", choices=["full", "headline", "copy", "decode"],
+                    default="full", help="headline/copy/decode: profiling runs")
+    ap.add_argument("--context", type=int, default=1024,
+                    help="first position of the timed decode steps")
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying a HIP graph")
     args = ap.parse_args()
@@ -322,6 +396,10 @@ def main():
         print(json.dumps({"mode": "copy", "bytes_read": COPY_BYTES,
                           "bytes_written": COPY_BYTES,
                           "us_per_copy": sec / args.steps * 1e6}), flush=True)
+        return
+    if args.mode == "decode":
+        r = bench_decode(pkg, torch, min(args.steps, 200), args.warmup, args.context)
+        print(json.dumps({"mode": "decode", **r}), flush=True)
         return
     head = bench_case(pkg, torch, "q4_0", 1, 18944, 3584, args.steps,
                       args.warmup, seed=1000, eager=args.eager)
@@ -361,6 +439,13 @@ def main():
                     "frac": round(prefill["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                     "dtype": "fp16 MFMA, fp32 accumulate"},
     }
+    try:
+        dec = bench_decode(pkg, torch, min(args.steps, 200), min(args.warmup, 5), args.context)
+        result["decode_step"] = {kk: (round(v, 4) if isinstance(v, float) else v)
+                                 for kk, v in dec.items()}
+    except Exception as e:  # reported, never fatal to the headline line
+        result["decode_step"] = {"error": f"{type(e).__name__}: {e}"}
+    torch.cuda.empty_cache()
     if args.all:
         extra = {}
         for name, qt, m, n, k in [("c0", "q8_0", 1, 4096, 4096),

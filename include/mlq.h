@@ -380,11 +380,14 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
                      void* ws, size_t ws_bytes, mlq_stream_t stream);
 
 /* Greedy sampling on the device (argMax, src/ops.cc:230-246, as the
- * sampler's temperature-0 choice): *token_dev = argmax(logits), then
- * *pos_dev += 1, so decode steps can follow each other with no host
- * round trip. */
+ * sampler's temperature-0 choice, MiniSampler::sampleGreedy,
+ * src/sampler.cc:109-114): *token_dev = argmax(logits), then *pos_dev += 1,
+ * so decode steps can follow each other with no host round trip. Two
+ * passes over slices of the logits; ws (device, 8-byte aligned, no
+ * initialisation) holds mlq_argmax_workspace(vocab) bytes. */
+int mlq_argmax_workspace(int64_t n, size_t* bytes);
 int mlq_greedy_next(const float* logits, int vocab, int32_t* token_dev, int32_t* pos_dev,
-                    mlq_stream_t stream);
+                    void* ws, size_t ws_bytes, mlq_stream_t stream);
 
 #ifdef __cplusplus
 }

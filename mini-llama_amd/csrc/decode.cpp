@@ -254,12 +254,22 @@ int mlq_argmax(const float* x, int64_t n, int32_t* out, mlq_stream_t stream) {
   return record_hip(launch_argmax(x, n, out, nullptr, (hipStream_t)stream));
 }
 
+int mlq_argmax_workspace(int64_t n, size_t* bytes) {
+  if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (n <= 0) return MLQ_ERR_SHAPE;
+  *bytes = argmax_workspace_bytes(n);
+  return MLQ_OK;
+}
+
 int mlq_greedy_next(const float* logits, int vocab, int32_t* token_dev, int32_t* pos_dev,
-                    mlq_stream_t stream) {
-  if (logits == nullptr || token_dev == nullptr || pos_dev == nullptr)
+                    void* ws, size_t ws_bytes, mlq_stream_t stream) {
+  if (logits == nullptr || token_dev == nullptr || pos_dev == nullptr || ws == nullptr)
     return MLQ_ERR_INVALID_ARG;
   if (vocab <= 0) return MLQ_ERR_SHAPE;
-  return record_hip(launch_argmax(logits, vocab, token_dev, pos_dev, (hipStream_t)stream));
+  if (((uintptr_t)ws & 7u) != 0) return MLQ_ERR_INVALID_ARG;
+  if (ws_bytes < argmax_workspace_bytes(vocab)) return MLQ_ERR_BUFFER_TOO_SMALL;
+  return record_hip(
+      launch_argmax_ws(logits, vocab, token_dev, pos_dev, ws, (hipStream_t)stream));
 }
 
 int mlq_decode_workspace(const mlq_model* m, size_t* bytes) {

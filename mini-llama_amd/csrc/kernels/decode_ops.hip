@@ -28,6 +28,42 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Reductions over the first N lanes of each 16-lane row with DPP (VALU
+// lane permutes, no LDS round trip): xor 1 and xor 2 as quad permutes, then
+// row_half_mirror (lane i <-> 7 - i: pairs the two quads of 8 lanes) and
+// row_mirror (i <-> 15 - i: pairs the two halves of the row). Every lane of
+// the N-lane group ends with the group's result.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int N>
+__device__ __forceinline__ float row_sum(float v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32, "row_sum width");
+  v += dpp<kDppXor1>(v);
+  if constexpr (N >= 4) v += dpp<kDppXor2>(v);
+  if constexpr (N >= 8) v += dpp<kDppHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp<kDppMirror>(v);
+  if constexpr (N >= 32) v += __shfl_xor(v, 16);
+  return v;
+}
+template <int N>
+__device__ __forceinline__ float row_max(float v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32, "row_max width");
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp<kDppXor2>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp<kDppMirror>(v));
+  if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  return v;
+}
+
 __device__ __forceinline__ int read_scalar(const int32_t* dev, int host) {
   return dev != nullptr ? *dev : host;
 }
@@ -54,6 +90,49 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
   const float scale = sqrtf(total / (float)dim + eps);
   for (int i = threadIdx.x; i < dim; i += kNormThreads)
     yr[i] = xr[i] * w[i] / scale;
+}
+
+// Row held in registers: R float4 of x and of the weight per thread, every
+// load issued before the reduction (one memory round trip), no second read. dim % 4 == 0 and
+// 16-byte aligned rows.
+template <int R>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_vec_kernel(
+    const float* __restrict__ x, const float* __restrict__ w,
+    float* __restrict__ y, int dim, float eps) {
+  __shared__ float part[kNormThreads / 64];
+  const int n4 = dim >> 2;
+  const f4_t* xr = (const f4_t*)(x + (size_t)blockIdx.x * dim);
+  f4_t* yr = (f4_t*)(y + (size_t)blockIdx.x * dim);
+  const f4_t* w4 = (const f4_t*)w;
+  f4_t v[R], wv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = threadIdx.x + r * kNormThreads;
+    v[r] = i < n4 ? xr[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    wv[r] = i < n4 ? w4[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    ss += v[r].x * v[r].x;
+    ss += v[r].y * v[r].y;
+    ss += v[r].z * v[r].z;
+    ss += v[r].w * v[r].w;
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) total += part[i];
+  const float scale = sqrtf(total / (float)dim + eps);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = threadIdx.x + r * kNormThreads;
+    if (i < n4)
+      yr[i] = f4_t{v[r].x * wv[r].x / scale, v[r].y * wv[r].y / scale,
+                   v[r].z * wv[r].z / scale, v[r].w * wv[r].w / scale};
+  }
 }
 
 // ---- elementwise ----------------------------------------------------------------
@@ -167,13 +246,23 @@ __global__ __launch_bounds__(256) void kv_write_kernel(float* __restrict__ keys,
 //   LDS slab. Partials (m, l, acc[hd]) go to the workspace.
 // Pass 2 (attn_combine_kernel): per query head, rescale the chunk partials to
 // the global max and divide by the global sum.
-// Positions per chunk: 64 (one per lane) for head dims up to 128; 32 for
-// larger or irregular head dims, which keeps the LDS slab under 64 KiB.
+// Two kernels share the partial format:
+//  - head_dim 64 / 128 / 256 (aligned buffers): attn_reg_kernel keeps its
+//    chunk in registers. L = hd/32 lanes share one position (32 dims of K
+//    each), so a wave covers P = 64/L positions (32, 16, 8) and issues every
+//    K and V load of the chunk before it uses any: one memory round trip
+//    per wave instead of one per row, 64 data registers per lane. Four
+//    waves per workgroup merge their partials in LDS, so a partial covers
+//    4P positions (128, 64, 32).
+//  - any other head_dim <= 256: attn_chunk_kernel stages 32-position chunks
+//    of K, then V, through LDS.
 constexpr int kAttnMaxGroup = 16;
 constexpr int kAttnMaxHd = 256;
-__host__ __device__ constexpr int attn_chunk_len(int hd) {
-  return (hd == 64 || hd == 128) ? 64 : 32;
-}
+constexpr int kAttnLdsChunk = 32;
+constexpr int kAttnRegWaves = 4;  // waves per workgroup of the register kernel
+__host__ __device__ constexpr bool attn_reg_hd(int hd) { return hd == 64 || hd == 128 || hd == 256; }
+// positions per workgroup: kAttnRegWaves waves of 64 * 32 / hd positions
+__host__ __device__ constexpr int attn_reg_chunk(int hd) { return kAttnRegWaves * 64 * 32 / hd; }
 
 struct AttnArgs {
   const float* q;       // [n_heads][hd]
@@ -190,7 +279,7 @@ struct AttnArgs {
 
 template <int HD, int GMAX>
 __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
-  constexpr int CH = attn_chunk_len(HD);
+  constexpr int CH = kAttnLdsChunk;
   const int hd = HD ? HD : a.hd;
   const int hdp = (hd + 3) & ~3;
   const int stride = hdp + 4;  // padded LDS row: ds_read_b128 by position lanes stays conflict-free
@@ -313,13 +402,169 @@ __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
   }
 }
 
+template <int HD, int GMAX>
+__global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a) {
+  constexpr int KD = 32;          // dims of K per lane
+  constexpr int L = HD / KD;      // lanes per position
+  constexpr int P = 64 / L;       // positions per wave
+  constexpr int KF = KD / 4;      // float4 of K per lane
+  constexpr int VJ = HD / 64;     // V dims per lane per position
+  constexpr int W = kAttnRegWaves;
+  __shared__ f4_t qs[GMAX * HD / 4];
+  __shared__ __align__(16) float ps[W][GMAX * P];
+  __shared__ float wm[W][GMAX], wl[W][GMAX];
+  __shared__ float wacc[W][GMAX][HD];
+
+  const int pos = read_scalar(a.pos_dev, a.pos);
+  const int len = pos + 1;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int tb = blockIdx.x * (W * P);  // first position of the workgroup
+  if (pos < 0 || pos >= a.max_seq || tb >= len) return;
+  const int t0 = tb + wave * P;         // first position of this wave
+  const int nt = max(0, min(P, len - t0));  // 0: an idle wave past the end
+  const int kvh = blockIdx.y;
+  const int G = a.group;
+  const int tp = lane % P;        // position of this lane in the wave's chunk
+  const int part = lane / P;      // which KD dims of K
+  const size_t row_stride = (size_t)a.n_kv * HD;
+  const size_t base = ((size_t)a.layer * a.max_seq + min(t0, len - 1)) * row_stride +
+                      (size_t)kvh * HD;
+  const int last = max(nt - 1, 0);
+
+  // every load of the chunk first: K piece, V columns, the group's q
+  const f4_t* kr = (const f4_t*)(a.keys + base + (size_t)min(tp, last) * row_stride + part * KD);
+  f4_t kreg[KF];
+#pragma unroll
+  for (int i = 0; i < KF; ++i) kreg[i] = kr[i];
+  float vreg[P][VJ];
+#pragma unroll
+  for (int t = 0; t < P; ++t)
+#pragma unroll
+    for (int j = 0; j < VJ; ++j)
+      vreg[t][j] = a.values[base + (size_t)min(t, last) * row_stride + j * 64 + lane];
+  // q of the group's heads; heads G..GMAX-1 are zero so every head loop
+  // below runs a fixed GMAX times with no per-head branches (their results
+  // are never stored), which lets the heads' reductions interleave
+  const f4_t* q4 = (const f4_t*)(a.q + (size_t)kvh * G * HD);
+  for (int i = threadIdx.x; i < GMAX * HD / 4; i += W * 64)
+    qs[i] = i < G * HD / 4 ? q4[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  __syncthreads();
+
+  // scores: this lane's KD dims, then the L parts summed across lanes
+  float s[GMAX];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    s[g] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KF; ++i) {
+      const f4_t qv = qs[(g * HD + part * KD) / 4 + i];
+      s[g] += qv.x * kreg[i].x;
+      s[g] += qv.y * kreg[i].y;
+      s[g] += qv.z * kreg[i].z;
+      s[g] += qv.w * kreg[i].w;
+    }
+  }
+#pragma unroll
+  for (int off = P; off < 64; off <<= 1)
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) s[g] += __shfl_xor(s[g], off);
+  // every part holds the full score now: reduce over the P positions only
+  // (P lanes of a 16-lane row, or two rows when P = 32)
+  const bool valid = tp < nt;
+  float m[GMAX], l[GMAX];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    const float sc = valid ? s[g] * a.scale : -INFINITY;
+    m[g] = row_max<P>(sc);  // an idle wave keeps m = -inf: it adds nothing below
+    s[g] = valid ? expf(sc - m[g]) : 0.0f;
+    l[g] = row_sum<P>(s[g]);
+  }
+  if (part == 0) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) ps[wave][g * P + tp] = s[g];
+  }
+  __syncthreads();
+
+  // acc[g][j] = sum_t p[g][t] * V[t][lane + 64 j], positions in order
+  float acc[GMAX][VJ];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) acc[g][j] = 0.0f;
+#pragma unroll
+  for (int t = 0; t < P; t += 4) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      const f4_t p4 = *(const f4_t*)&ps[wave][g * P + t];
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) {
+        acc[g][j] += p4.x * vreg[t][j];
+        acc[g][j] += p4.y * vreg[t + 1][j];
+        acc[g][j] += p4.z * vreg[t + 2][j];
+        acc[g][j] += p4.w * vreg[t + 3][j];
+      }
+    }
+  }
+  // the workgroup's W wave partials merged in wave order into one
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    if (g < G) {
+      if (lane == 0) {
+        wm[wave][g] = m[g];
+        wl[wave][g] = l[g];
+      }
+#pragma unroll
+      for (int j = 0; j < VJ; ++j) wacc[wave][g][j * 64 + lane] = acc[g][j];
+    }
+  }
+  __syncthreads();
+  const int chunk = blockIdx.x;
+  const int n_heads = G * a.n_kv;
+  float* pm = a.part;
+  float* pl = a.part + (size_t)n_heads * a.chunks;
+  float* pa = pl + (size_t)n_heads * a.chunks;
+  for (int g = wave; g < G; g += W) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, wm[w][g]);
+    float f[W];
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      f[w] = wm[w][g] == -INFINITY ? 0.0f : expf(wm[w][g] - mx);
+      sum += wl[w][g] * f[w];
+    }
+    const size_t slot = (size_t)(kvh * G + g) * a.chunks + chunk;
+    if (lane == 0) {
+      pm[slot] = mx;
+      pl[slot] = sum;
+    }
+#pragma unroll
+    for (int j = 0; j < VJ; ++j) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) v += wacc[w][g][j * 64 + lane] * f[w];
+      pa[slot * HD + j * 64 + lane] = v;
+    }
+  }
+}
+
+// Pass 2: one wave per query head. Lanes take chunks for the global max and
+// the rescaled sum; the weights exp(m_c - M) go through LDS 32 chunks at a
+// time, and lanes over head dims load those 32 partials at once (predicated,
+// so one memory round trip per batch) and sum them in chunk order.
+constexpr int kCombineBatch = 32;
+
 __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
+  __shared__ float wsh[kCombineBatch];
   const int pos = read_scalar(a.pos_dev, a.pos);
   const int head = blockIdx.x;
+  const int lane = threadIdx.x;
   const int n_heads = a.group * a.n_kv;
   float* out = a.out + (size_t)head * a.hd;
   if (pos < 0 || pos >= a.max_seq) {  // only reachable through a device position
-    for (int d = threadIdx.x; d < a.hd; d += 64) out[d] = __builtin_nanf("");
+    for (int d = lane; d < a.hd; d += 64) out[d] = __builtin_nanf("");
     return;
   }
   const int chunks = (pos + a.chunk_len) / a.chunk_len;
@@ -327,13 +572,37 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   const float* pl = a.part + (size_t)n_heads * a.chunks + (size_t)head * a.chunks;
   const float* pa = a.part + 2 * (size_t)n_heads * a.chunks + (size_t)head * a.chunks * a.hd;
   float mx = -INFINITY;
-  for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, pm[c]);
+  for (int c = lane; c < chunks; c += 64) mx = fmaxf(mx, pm[c]);
+  mx = wave_max(mx);
   float denom = 0.0f;
-  for (int c = 0; c < chunks; ++c) denom += pl[c] * expf(pm[c] - mx);
-  for (int d = threadIdx.x; d < a.hd; d += 64) {
-    float acc = 0.0f;
-    for (int c = 0; c < chunks; ++c) acc += pa[(size_t)c * a.hd + d] * expf(pm[c] - mx);
-    out[d] = acc / denom;
+  for (int c = lane; c < chunks; c += 64) denom += pl[c] * expf(pm[c] - mx);
+  denom = wave_sum(denom);
+  constexpr int kD = kAttnMaxHd / 64;
+  float acc[kD];
+#pragma unroll
+  for (int j = 0; j < kD; ++j) acc[j] = 0.0f;
+  for (int c0 = 0; c0 < chunks; c0 += kCombineBatch) {
+    const int nc = min(kCombineBatch, chunks - c0);
+    __syncthreads();
+    if (lane < kCombineBatch) wsh[lane] = lane < nc ? expf(pm[c0 + lane] - mx) : 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kD; ++j) {
+      const int d = lane + 64 * j;
+      if (d < a.hd) {
+        const float* col = pa + (size_t)c0 * a.hd + d;
+        float v[kCombineBatch];
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u) v[u] = u < nc ? col[(size_t)u * a.hd] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u) acc[j] += v[u] * wsh[u];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kD; ++j) {
+    const int d = lane + 64 * j;
+    if (d < a.hd) out[d] = acc[j] / denom;
   }
 }
 
@@ -352,11 +621,21 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
   __shared__ int64_t si[kArgmaxThreads / 64];
   float best = -INFINITY;
   int64_t idx = INT64_MAX;
-  for (int64_t i = threadIdx.x; i < n; i += kArgmaxThreads) {
-    const float v = x[i];
-    if (v > best || (idx == INT64_MAX && v == best)) {
-      best = v;
-      idx = i;
+  constexpr int kU = 8;  // independent loads in flight per thread
+  for (int64_t b = 0; b < n; b += (int64_t)kArgmaxThreads * kU) {
+    float v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t i = b + threadIdx.x + (int64_t)u * kArgmaxThreads;
+      v[u] = i < n ? x[i] : __builtin_nanf("");
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t i = b + threadIdx.x + (int64_t)u * kArgmaxThreads;
+      if (v[u] > best || (idx == INT64_MAX && v[u] == best)) {
+        best = v[u];
+        idx = i;
+      }
     }
   }
 #pragma unroll
@@ -387,13 +666,91 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
   }
 }
 
+// Two-pass form for long vectors (the vocabulary): pass 1 gives each
+// workgroup kArgmaxSlice consecutive elements (16 independent loads per
+// thread), pass 2 merges the per-workgroup (value, index) pairs in order.
+constexpr int kArgmaxSliceThreads = 256;
+constexpr int kArgmaxPerThread = 16;
+constexpr int kArgmaxSlice = kArgmaxSliceThreads * kArgmaxPerThread;
+
+__device__ __forceinline__ void argmax_merge(float& best, int64_t& idx, float ov, int64_t oi) {
+  if (ov > best || (ov == best && oi < idx)) {
+    best = ov;
+    idx = oi;
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void argmax_block(float& best, int64_t& idx) {
+  __shared__ float sv[NT / 64];
+  __shared__ int64_t si[NT / 64];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    argmax_merge(best, idx, __shfl_xor(best, off), __shfl_xor(idx, off));
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = best;
+    si[threadIdx.x >> 6] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int w = 1; w < NT / 64; ++w) argmax_merge(best, idx, sv[w], si[w]);
+}
+
+__global__ __launch_bounds__(kArgmaxSliceThreads) void argmax_partial_kernel(
+    const float* __restrict__ x, int64_t n, float* pv, int64_t* pi) {
+  const int64_t b0 = (int64_t)blockIdx.x * kArgmaxSlice;
+  float v[kArgmaxPerThread];
+#pragma unroll
+  for (int u = 0; u < kArgmaxPerThread; ++u) {
+    const int64_t i = b0 + threadIdx.x + (int64_t)u * kArgmaxSliceThreads;
+    v[u] = i < n ? x[i] : __builtin_nanf("");
+  }
+  float best = -INFINITY;
+  int64_t idx = INT64_MAX;
+#pragma unroll
+  for (int u = 0; u < kArgmaxPerThread; ++u) {
+    const int64_t i = b0 + threadIdx.x + (int64_t)u * kArgmaxSliceThreads;
+    if (v[u] > best || (idx == INT64_MAX && v[u] == best)) {
+      best = v[u];
+      idx = i;
+    }
+  }
+  argmax_block<kArgmaxSliceThreads>(best, idx);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = best;
+    pi[blockIdx.x] = idx;
+  }
+}
+
+__global__ __launch_bounds__(kArgmaxSliceThreads) void argmax_final_kernel(
+    const float* __restrict__ pv, const int64_t* __restrict__ pi, int parts,
+    const float* __restrict__ x, int32_t* out, int32_t* pos_dev) {
+  float best = -INFINITY;
+  int64_t idx = INT64_MAX;
+  for (int b = threadIdx.x; b < parts; b += kArgmaxSliceThreads) argmax_merge(best, idx, pv[b], pi[b]);
+  argmax_block<kArgmaxSliceThreads>(best, idx);
+  if (threadIdx.x == 0) {
+    if (isnan(x[0]) || idx == INT64_MAX) idx = 0;
+    *out = (int32_t)idx;
+    if (pos_dev != nullptr) *pos_dev += 1;
+  }
+}
+
 }  // namespace
 
 // ---- launchers ---------------------------------------------------------------------
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim,
                           float eps, hipStream_t stream) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, stream, x, w, y,
-                     dim, eps);
+  const bool vec = dim % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+                   ((uintptr_t)y & 15) == 0;
+  const int per = (dim / 4 + kNormThreads - 1) / kNormThreads;  // float4 per thread
+  const dim3 grid(rows), block(kNormThreads);
+  if (vec && per <= 1) hipLaunchKernelGGL(rmsnorm_vec_kernel<1>, grid, block, 0, stream, x, w, y, dim, eps);
+  else if (vec && per <= 2) hipLaunchKernelGGL(rmsnorm_vec_kernel<2>, grid, block, 0, stream, x, w, y, dim, eps);
+  else if (vec && per <= 4) hipLaunchKernelGGL(rmsnorm_vec_kernel<4>, grid, block, 0, stream, x, w, y, dim, eps);
+  else if (vec && per <= 8) hipLaunchKernelGGL(rmsnorm_vec_kernel<8>, grid, block, 0, stream, x, w, y, dim, eps);
+  else if (vec && per <= 16) hipLaunchKernelGGL(rmsnorm_vec_kernel<16>, grid, block, 0, stream, x, w, y, dim, eps);
+  else hipLaunchKernelGGL(rmsnorm_kernel, grid, block, 0, stream, x, w, y, dim, eps);
   return hipGetLastError();
 }
 
@@ -451,8 +808,10 @@ hipError_t launch_kv_write(float* keys, float* values, const float* k, const flo
   return hipGetLastError();
 }
 
+// Chunk count the workspace is sized for: the shorter chunk of the two
+// kernels a head dim can take (the register kernel needs aligned buffers).
 int attention_chunks(int hd, int max_len) {
-  const int ch = attn_chunk_len(hd == 64 || hd == 128 ? hd : 0);
+  const int ch = attn_reg_hd(hd) ? min(attn_reg_chunk(hd), kAttnLdsChunk) : kAttnLdsChunk;
   return (max_len + ch - 1) / ch;
 }
 
@@ -467,22 +826,26 @@ bool attention_supported(int n_heads, int n_kv, int hd) {
 }
 
 template <int HD, int GMAX>
-static void attn_launch(const AttnArgs& a, int chunks, hipStream_t stream) {
-  constexpr int CH = attn_chunk_len(HD);
-  const int hd = HD ? HD : a.hd;
-  const int hdp = (hd + 3) & ~3;
-  const size_t lds = (size_t)(CH * (hdp + 4) + GMAX * hdp + GMAX * CH) * sizeof(float);
-  hipLaunchKernelGGL((attn_chunk_kernel<HD, GMAX>), dim3(chunks, a.n_kv), dim3(64), lds,
-                     stream, a);
+static void attn_launch(const AttnArgs& a, hipStream_t stream) {
+  if constexpr (HD != 0) {
+    hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX>), dim3(a.chunks, a.n_kv),
+                       dim3(kAttnRegWaves * 64), 0, stream, a);
+  } else {
+    constexpr int CH = kAttnLdsChunk;
+    const int hdp = (a.hd + 3) & ~3;
+    const size_t lds = (size_t)(CH * (hdp + 4) + GMAX * hdp + GMAX * CH) * sizeof(float);
+    hipLaunchKernelGGL((attn_chunk_kernel<0, GMAX>), dim3(a.chunks, a.n_kv), dim3(64), lds,
+                       stream, a);
+  }
 }
 
 template <int HD>
-static void attn_launch_g(const AttnArgs& a, int chunks, hipStream_t stream) {
-  if (a.group <= 1) attn_launch<HD, 1>(a, chunks, stream);
-  else if (a.group <= 2) attn_launch<HD, 2>(a, chunks, stream);
-  else if (a.group <= 4) attn_launch<HD, 4>(a, chunks, stream);
-  else if (a.group <= 8) attn_launch<HD, 8>(a, chunks, stream);
-  else attn_launch<HD, 16>(a, chunks, stream);
+static void attn_launch_g(const AttnArgs& a, hipStream_t stream) {
+  if (a.group <= 1) attn_launch<HD, 1>(a, stream);
+  else if (a.group <= 2) attn_launch<HD, 2>(a, stream);
+  else if (a.group <= 4) attn_launch<HD, 4>(a, stream);
+  else if (a.group <= 8) attn_launch<HD, 8>(a, stream);
+  else if constexpr (HD != 64) attn_launch<HD, 16>(a, stream);
 }
 
 hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
@@ -497,18 +860,21 @@ hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   a.n_kv = r.n_kv;
   a.hd = r.hd;
   a.group = r.n_heads / r.n_kv;
-  a.chunks = attention_chunks(r.hd, r.max_len);
-  a.chunk_len = attn_chunk_len(r.hd == 64 || r.hd == 128 ? r.hd : 0);
   a.vec = r.hd % 4 == 0 && ((uintptr_t)r.keys & 15) == 0 && ((uintptr_t)r.values & 15) == 0;
+  // (head_dim 64 with more than 8 query heads per kv head would spill the
+  // register kernel: it takes the LDS kernel)
+  const bool reg = attn_reg_hd(r.hd) && a.vec && ((uintptr_t)r.q & 15) == 0 &&
+                   !(r.hd == 64 && a.group > 8);
+  a.chunk_len = reg ? attn_reg_chunk(r.hd) : kAttnLdsChunk;
+  a.chunks = (r.max_len + a.chunk_len - 1) / a.chunk_len;
   a.pos_dev = r.pos_dev;
   a.pos = r.pos;
   a.scale = sqrtf(1.0f / (float)r.hd);
-  const int chunks = a.chunks;
-  switch (r.hd) {
-    case 64: attn_launch_g<64>(a, chunks, stream); break;
-    case 128: attn_launch_g<128>(a, chunks, stream); break;
-    case 256: attn_launch_g<256>(a, chunks, stream); break;
-    default: attn_launch_g<0>(a, chunks, stream); break;
+  switch (reg ? r.hd : 0) {
+    case 64: attn_launch_g<64>(a, stream); break;
+    case 128: attn_launch_g<128>(a, stream); break;
+    case 256: attn_launch_g<256>(a, stream); break;
+    default: attn_launch_g<0>(a, stream); break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -520,6 +886,25 @@ hipError_t launch_argmax(const float* x, int64_t n, int32_t* out, int32_t* pos_d
                          hipStream_t stream) {
   hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxThreads), 0, stream, x, n, out,
                      pos_dev);
+  return hipGetLastError();
+}
+
+size_t argmax_workspace_bytes(int64_t n) {
+  const size_t parts = (size_t)((n + kArgmaxSlice - 1) / kArgmaxSlice);
+  return parts * (sizeof(float) + sizeof(int64_t)) + 16;
+}
+
+hipError_t launch_argmax_ws(const float* x, int64_t n, int32_t* out, int32_t* pos_dev,
+                            void* ws, hipStream_t stream) {
+  const int parts = (int)((n + kArgmaxSlice - 1) / kArgmaxSlice);
+  int64_t* pi = (int64_t*)ws;
+  float* pv = (float*)(pi + parts);
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(parts), dim3(kArgmaxSliceThreads), 0, stream,
+                     x, n, pv, pi);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgmaxSliceThreads), 0, stream, pv, pi,
+                     parts, x, out, pos_dev);
   return hipGetLastError();
 }
 

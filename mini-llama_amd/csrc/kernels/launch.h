@@ -123,7 +123,13 @@ int attention_chunks(int hd, int max_len);
 size_t attention_workspace_bytes(int n_heads, int hd, int max_len);
 hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream);
 // out = argmax(x) (first maximum, NaN never wins); pos_dev += 1 when non-null.
+// One workgroup, no workspace:
 hipError_t launch_argmax(const float* x, int64_t n, int32_t* out, int32_t* pos_dev,
                          hipStream_t stream);
+// Two passes over slices of the vector with argmax_workspace_bytes(n) of
+// 8-byte-aligned scratch:
+size_t argmax_workspace_bytes(int64_t n);
+hipError_t launch_argmax_ws(const float* x, int64_t n, int32_t* out, int32_t* pos_dev,
+                            void* ws, hipStream_t stream);
 
 }  // namespace mlq

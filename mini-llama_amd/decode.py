@@ -10,7 +10,9 @@ A model is a plain dict (the same format the CPU oracle reads):
    "layers": [{"attention_norm", "wq", "wk", "wv", "bq"?, "bk"?, "bv"?, "wo",
                "ffn_norm", "w_gate", "w_up", "w_down"}, ...]}
 with every projection W = {"type": "f32" | "q8_0" | "q4_0" | "q4_1",
-"shape": (n, k), "data": fp32 [n, k] or GGUF blocks}.
+"shape": (n, k), "data": fp32 [n, k] or GGUF blocks}. Arrays may be numpy
+(uploaded; quantized blocks repacked on the host) or torch device tensors
+(quantized blocks as raw bytes, repacked by the device kernel).
 
 DecodeModel uploads it once. Where the types allow it, q|k|v become one
 concatenated weight (one GEMV with the concatenated bias fused) and
@@ -30,22 +32,45 @@ import os
 import numpy as np
 
 from . import (MlqKvCache, MlqLayer, MlqModel, MlqWeight, TiledWeight, _check, _stream,
-               interleave_rows, lib, upload, upload_concat, upload_f32, upload_glu)
+               interleave_rows, lib, repack_device, upload, upload_concat, upload_f32,
+               upload_glu, weight_layout)
 
 CONFIG_KEYS = ("vocab_size", "dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads",
                "head_dim", "max_seq_len")
 
 
+def _on_device(a) -> bool:
+    return hasattr(a, "is_cuda") and a.is_cuda
+
+
+def _device_linear(qtype: str, data, n: int, k: int) -> TiledWeight:
+    """A weight whose data already lives on the device: fp32 [n, k] used as
+    is, GGUF blocks (uint8 bytes) repacked by the device kernel."""
+    import torch
+    raw = data.contiguous().view(-1).view(torch.uint8)
+    if qtype == "f32":
+        return TiledWeight("f32", n, k, raw, weight_layout("f32", n, k))
+    return repack_device(qtype, raw, n, k)
+
+
 def _upload_linear(w: dict, device) -> TiledWeight:
     n, k = w["shape"]
+    if _on_device(w["data"]):
+        return _device_linear(w["type"], w["data"], n, k)
     if w["type"] == "f32":
         return upload_f32(np.asarray(w["data"], np.float32).reshape(n, k), device=device)
     return upload(w["type"], w["data"], n, k, device=device)
 
 
 def _upload_rows(ws: list, device) -> TiledWeight:
-    """Row concatenation of weights of one type sharing in_features."""
+    """Row concatenation of weights of one type sharing in_features (GGUF
+    block rows or fp32 rows concatenate as bytes)."""
     k = ws[0]["shape"][1]
+    n = sum(w["shape"][0] for w in ws)
+    if _on_device(ws[0]["data"]):
+        import torch
+        cat = torch.cat([w["data"].contiguous().view(torch.uint8).reshape(-1) for w in ws])
+        return _device_linear(ws[0]["type"], cat, n, k)
     if ws[0]["type"] == "f32":
         return upload_f32(np.concatenate([np.asarray(w["data"], np.float32).reshape(w["shape"])
                                           for w in ws]), device=device)
@@ -56,6 +81,13 @@ def _upload_rows(ws: list, device) -> TiledWeight:
 
 def _upload_gate_up(gate: dict, up: dict, device) -> TiledWeight:
     hid, k = gate["shape"]
+    if _on_device(gate["data"]):
+        # rows 16t..16t+7 = gate rows 8t..8t+7, 16t+8..16t+15 = up rows (as
+        # mlq_interleave_rows), done on the device's row bytes
+        import torch
+        g = gate["data"].contiguous().view(torch.uint8).reshape(hid // 8, 8, -1)
+        u = up["data"].contiguous().view(torch.uint8).reshape(hid // 8, 8, -1)
+        return _device_linear(gate["type"], torch.stack([g, u], dim=1).reshape(-1), 2 * hid, k)
     if gate["type"] == "f32":
         g = np.asarray(gate["data"], np.float32).reshape(hid, k)
         u = np.asarray(up["data"], np.float32).reshape(hid, k)
@@ -76,7 +108,10 @@ class DecodeModel:
         self._keep = []  # device tensors and weights referenced by the structs
 
         def dev(a) -> int:
-            t = torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(self.device)
+            if _on_device(a):
+                t = a.to(self.device, torch.float32).contiguous()
+            else:
+                t = torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(self.device)
             self._keep.append(t)
             return t.data_ptr()
 
@@ -95,6 +130,7 @@ class DecodeModel:
             qkv = [lw["wq"], lw["wk"], lw["wv"]]
             fuse_qkv = fuse and len({w["type"] for w in qkv}) == 1
             biases = [lw.get(b) for b in ("bq", "bk", "bv")]
+            biases = [b.cpu().numpy() if _on_device(b) else b for b in biases]
             if fuse_qkv:
                 L.wq = weight(_upload_rows(qkv, self.device))
                 if any(b is not None and np.size(b) for b in biases):
@@ -143,6 +179,9 @@ class DecodeModel:
         self.logits = torch.empty(c["vocab_size"], dtype=torch.float32, device=self.device)
         self.token_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.pos_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
+        _check(lib().mlq_argmax_workspace(c["vocab_size"], ctypes.byref(nbytes)),
+               "mlq_argmax_workspace")
+        self.argmax_ws = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
 
     @property
     def weight_bytes(self) -> int:
@@ -175,8 +214,12 @@ class DecodeModel:
                                       0, 0, self.token_dev.data_ptr(), self.pos_dev.data_ptr(),
                                       self.logits.data_ptr(), ws.data_ptr(), ws.numel(), s),
                "mlq_decode_token")
+        self._greedy(s)
+
+    def _greedy(self, s) -> None:
         _check(lib().mlq_greedy_next(self.logits.data_ptr(), self.config["vocab_size"],
-                                     self.token_dev.data_ptr(), self.pos_dev.data_ptr(), s),
+                                     self.token_dev.data_ptr(), self.pos_dev.data_ptr(),
+                                     self.argmax_ws.data_ptr(), self.argmax_ws.numel(), s),
                "mlq_greedy_next")
 
     def greedy_graph(self):
@@ -209,9 +252,7 @@ class DecodeModel:
         for i, t in enumerate(prompt):
             self.forward_token(t, i)
         self.pos_dev.fill_(len(prompt) - 1)
-        _check(lib().mlq_greedy_next(self.logits.data_ptr(), self.config["vocab_size"],
-                                     self.token_dev.data_ptr(), self.pos_dev.data_ptr(),
-                                     _stream(None)), "mlq_greedy_next")
+        self._greedy(_stream(None))
         history = torch.empty(n_new, dtype=torch.int32, device=self.device)
         history[0:1].copy_(self.token_dev)
         g = self.greedy_graph() if graph and n_new > 1 else None

@@ -116,3 +116,63 @@ def synthetic_model(config: dict, qtype: str = "q4_0", seed: int = 0,
             "final_norm": norm(),
             "lm_head": _linear(lm_head_type or qtype, c["vocab_size"], dim, seed * 1000 + 999),
             "layers": layers}
+
+
+def _device_blocks(torch, gen, qtype: str, n: int, k: int, rms: float, device):
+    """GGUF block bytes made on the device (same distributions as
+    make_blocks_scaled), [n * ceil(k/32) * block bytes] uint8."""
+    count = n * ((k + 31) // 32)
+    d = (torch.randn(count, generator=gen, device=device) * (rms / _CODE_RMS[qtype])).abs()
+    d16 = d.half()
+    parts = [d16.view(torch.uint8).reshape(count, 2)]
+    if qtype == "q4_1":
+        parts.append((-7.5 * d16.float()).half().view(torch.uint8).reshape(count, 2))
+    if qtype == "q8_0":
+        qs = torch.randint(-127, 128, (count, 32), generator=gen, device=device,
+                           dtype=torch.int16).to(torch.int8).view(torch.uint8)
+    else:
+        qs = torch.randint(0, 256, (count, 16), generator=gen, device=device,
+                           dtype=torch.int16).to(torch.uint8)
+    parts.append(qs)
+    return torch.cat(parts, dim=1).reshape(-1)
+
+
+def synthetic_model_device(config: dict, qtype: str = "q4_0", seed: int = 0,
+                           bias: bool = False, device: str = "cuda") -> dict:
+    """synthetic_model with every array generated on the device (torch),
+    for models too large to build on the host quickly (a 7B decoder is
+    ~4 GB of q4_0 blocks plus a 2 GB fp32 embedding table)."""
+    import torch
+    c = dict(config)
+    c.setdefault("head_dim", c["dim"] // c["n_heads"])
+    c.setdefault("rope_theta", 10000.0)
+    c.setdefault("rms_norm_eps", 1e-5)
+    c.setdefault("rope_type", 0)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    dim, hid, hd = c["dim"], c["hidden_dim"], c["head_dim"]
+    qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
+
+    def lin(n, k):
+        rms = 1.0 / float(np.sqrt(k))
+        if qtype == "f32":
+            return {"type": "f32", "shape": (n, k),
+                    "data": torch.randn(n, k, generator=gen, device=device) * rms}
+        return {"type": qtype, "shape": (n, k),
+                "data": _device_blocks(torch, gen, qtype, n, k, rms, device)}
+
+    def norm():
+        return 1.0 + 0.1 * torch.randn(dim, generator=gen, device=device)
+
+    layers = []
+    for _ in range(c["n_layers"]):
+        layer = {"attention_norm": norm(), "wq": lin(qd, dim), "wk": lin(kvd, dim),
+                 "wv": lin(kvd, dim), "wo": lin(dim, qd), "ffn_norm": norm(),
+                 "w_gate": lin(hid, dim), "w_up": lin(hid, dim), "w_down": lin(dim, hid)}
+        if bias:
+            for name, n in (("bq", qd), ("bk", kvd), ("bv", kvd)):
+                layer[name] = 0.1 * torch.randn(n, generator=gen, device=device)
+        layers.append(layer)
+    return {"config": c,
+            "token_embedding": torch.randn(c["vocab_size"], dim, generator=gen, device=device),
+            "final_norm": norm(), "lm_head": lin(c["vocab_size"], dim), "layers": layers}

@@ -44,7 +44,9 @@ def test_operator_validation(pkg):
     assert lib.mlq_rope(FAKE, FAKE, 4, 2, 8, 0, float("inf"), 0, None) == -1
     assert lib.mlq_rope(FAKE, FAKE, 4, 2, 8, 0, 1e4, 2, None) == -1
     assert lib.mlq_argmax(FAKE, 0, FAKE, None) == -2
-    assert lib.mlq_greedy_next(FAKE, 10, None, FAKE, None) == -1
+    assert lib.mlq_greedy_next(FAKE, 10, None, FAKE, FAKE, 1 << 20, None) == -1
+    assert lib.mlq_greedy_next(FAKE, 10, FAKE, FAKE, FAKE, 8, None) == -4
+    assert lib.mlq_greedy_next(FAKE, 10, FAKE, FAKE, FAKE + 4, 1 << 20, None) == -1
 
 
 def test_cache_and_attention_validation(pkg):
@@ -54,8 +56,14 @@ def test_cache_and_attention_validation(pkg):
     assert nbytes.value == 28 * 4096 * 4 * 128 * 4
     c = pkg.MlqKvCache(FAKE, FAKE, 2, 64, 4, 128)
     assert lib.mlq_attention_workspace(ctypes.byref(c), 28, ctypes.byref(nbytes)) == 0
-    # m, l and hd partials per (query head, 64-position chunk)
-    assert nbytes.value == 28 * 1 * (2 + 128) * 4
+    # m, l and hd partials per (query head, chunk of 32 positions): the
+    # register kernel's workgroups cover 128 / 64 / 32 positions at head_dim
+    # 64 / 128 / 256, the LDS kernel 32
+    assert nbytes.value == 28 * 2 * (2 + 128) * 4
+    for hd, chunk in ((64, 32), (256, 32), (80, 32), (8, 32)):
+        ch = pkg.MlqKvCache(FAKE, FAKE, 2, 64, 4, hd)
+        assert lib.mlq_attention_workspace(ctypes.byref(ch), 8, ctypes.byref(nbytes)) == 0
+        assert nbytes.value == 8 * (64 // chunk) * (2 + hd) * 4
     assert lib.mlq_attention_workspace(ctypes.byref(c), 30, ctypes.byref(nbytes)) == -2
     assert lib.mlq_attention_workspace(ctypes.byref(c), 4 * 17, ctypes.byref(nbytes)) == -5
     big = pkg.MlqKvCache(FAKE, FAKE, 1, 8, 1, 512)
@@ -116,7 +124,7 @@ def test_decode_workspace_plan(pkg):
         m, _ = _fake_model(pkg, QWEN2_7B, fuse_qkv=fq, fuse_glu=fg)
         assert lib.mlq_decode_workspace(ctypes.byref(m), ctypes.byref(nbytes)) == 0
         # activations (a few hundred KiB) + attention partials for 4096 positions
-        attn = 28 * 64 * (2 + 128) * 4
+        attn = 28 * (4096 // 32) * (2 + 128) * 4
         assert attn <= nbytes.value <= attn + (1 << 20)
     m, layers = _fake_model(pkg, QWEN2_7B)
     layers[3].wo.n = 3583

@@ -231,6 +231,35 @@ def test_attention_matches_oracle(pkg, oracle, cuda, n_heads, n_kv, hd, max_seq,
                                atol=1e-5)
 
 
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_attention_unaligned_buffers(pkg, oracle, cuda, hd):
+    """Caches and q that are not 16-byte aligned take the LDS-staged kernel
+    (the register kernel loads float4): same results."""
+    import torch
+    n_heads, n_kv, max_seq, pos = 8, 2, 100, 77
+    rng = np.random.default_rng(hd)
+    keys = rng.standard_normal((1, max_seq, n_kv, hd)).astype(np.float32)
+    values = rng.standard_normal((1, max_seq, n_kv, hd)).astype(np.float32)
+    q = (rng.standard_normal((n_heads, hd)) * 0.5).astype(np.float32)
+    kbuf = torch.zeros(keys.size + 1, device=cuda)
+    vbuf = torch.zeros(values.size + 1, device=cuda)
+    kbuf[1:] = torch.from_numpy(keys.reshape(-1)).to(cuda)
+    vbuf[1:] = torch.from_numpy(values.reshape(-1)).to(cuda)
+    c = pkg.MlqKvCache(kbuf[1:].data_ptr(), vbuf[1:].data_ptr(), 1, max_seq, n_kv, hd)
+    lib = pkg.lib()
+    nbytes = ctypes.c_size_t()
+    _ok(pkg, lib.mlq_attention_workspace(ctypes.byref(c), n_heads, ctypes.byref(nbytes)), "ws")
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=cuda)
+    qbuf = torch.zeros(q.size + 1, device=cuda)
+    qbuf[1:] = torch.from_numpy(q.reshape(-1)).to(cuda)
+    out = torch.empty((n_heads, hd), device=cuda)
+    _ok(pkg, lib.mlq_attention_decode(ctypes.byref(c), 0, pos, qbuf[1:].data_ptr(), n_heads,
+                                      out.data_ptr(), ws.data_ptr(), ws.numel(), _s(pkg)),
+        "attention")
+    np.testing.assert_allclose(out.cpu().numpy(), oracle.attention(q, keys, values, 0, pos),
+                               rtol=1e-4, atol=1e-5)
+
+
 def test_attention_validation(pkg, cuda):
     # tests/test_cuda.cc:1143-1184: shape, layer, position, divisibility checks
     cache = Cache(pkg, cuda, 1, 8, 2, 4)
@@ -378,6 +407,41 @@ def test_synthetic_models_match_oracle(pkg, oracle, cuda, qtype, kw, fuse):
     tokens = rng.integers(0, cfg["vocab_size"], 70).tolist()  # crosses a 64-position chunk
     _, worst = _run_both(pkg, oracle, model, tokens, fuse=fuse)
     print(f"{qtype} {kw} fuse={fuse}: worst logits error / max|logit| = {worst:.2e}")
+
+
+def _to_host(x):
+    if isinstance(x, dict):
+        return {k: _to_host(v) for k, v in x.items()}
+    if isinstance(x, list):
+        return [_to_host(v) for v in x]
+    if hasattr(x, "is_cuda"):
+        return x.cpu().numpy()
+    return x
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0", "q4_1", "f32"])
+def test_device_built_model_matches_oracle(pkg, oracle, cuda, qtype):
+    """A model generated on the device (device repack, device q|k|v
+    concatenation and gate|up interleave) against the oracle on the same
+    bytes brought to the host."""
+    import mini_llama_amd.decode as dec
+    import mini_llama_amd.synth as synth
+    cfg = dict(vocab_size=128, dim=128, hidden_dim=192, n_layers=2, n_heads=8, n_kv_heads=2,
+               max_seq_len=32, rope_type=1)
+    dmodel = synth.synthetic_model_device(cfg, qtype, seed=4, bias=True)
+    host = _to_host(dmodel)
+    for lw in host["layers"] + [host]:
+        for name in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down", "lm_head"):
+            w = lw.get(name)
+            if w is not None and qtype != "f32":
+                w["data"] = w["data"].view(oracle.BLOCK_DTYPES[qtype])
+    dm = dec.DecodeModel(dmodel)
+    assert all(dm.fused_qkv) and all(dm.fused_glu)
+    cache = oracle.new_cache(host)
+    for pos, t in enumerate([5, 77, 1, 127, 64]):
+        ref = oracle.forward_token(host, cache, t, pos)
+        got = dm.forward_token(t, pos).cpu().numpy()
+        assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max() + 1e-6, pos
 
 
 def test_qwen2_7b_layer_at_full_size(pkg, oracle, cuda):
