@@ -306,6 +306,23 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     return mlq_linear_epi(&w, x, y, 1, bias, act, b.lin, b.lin_bytes, stream);
   };
   auto hip = [](hipError_t e) { return record_hip(e); };
+  // Linear of rmsNorm(x, norm): folded into the decode GEMV's activation
+  // staging when that kernel runs the weight (quantized, one row), else a
+  // separate RMSNorm pass into b.h first.
+  auto norm_linear = [&](const mlq_weight& w, const float* x, const float* norm, float* y,
+                         const float* bias, int act) {
+    if (w.type != MLQ_F32 && w.k <= gemv_max_k(w.type, 1) && gemv_norm_supported(w)) {
+      Epilogue e;
+      e.bias = bias;
+      e.act = act == MLQ_EPI_SWIGLU ? kEpiSwiGLU : kEpiNone;
+      e.norm = norm;
+      e.norm_eps = m->rms_norm_eps;
+      return hip(launch_gemv(w, x, y, 1, s, e));
+    }
+    int rc = hip(launch_rmsnorm(x, norm, b.h, 1, dim, m->rms_norm_eps, s));
+    if (rc != MLQ_OK) return rc;
+    return linear(w, b.h, y, bias, act);
+  };
 
   if ((rc = hip(launch_embedding(m->token_embedding, m->vocab_size, dim, token_dev, token,
                                  b.x, s))) != MLQ_OK)
@@ -313,14 +330,17 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
   for (int li = 0; li < m->n_layers; ++li) {
     const mlq_layer& l = m->layers[li];
     // attention sublayer (forwardLayerDevice, src/forward.cc:607-640)
-    if ((rc = hip(launch_rmsnorm(b.x, l.attn_norm, b.h, 1, dim, m->rms_norm_eps, s))) != MLQ_OK)
-      return rc;
     if (qkv_fused(l)) {
-      if ((rc = linear(l.wq, b.h, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = norm_linear(l.wq, b.x, l.attn_norm, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK)
+        return rc;
     } else {
-      if ((rc = linear(l.wq, b.h, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK) return rc;
-      if ((rc = linear(l.wk, b.h, b.qkv + qd, l.bk, MLQ_EPI_NONE)) != MLQ_OK) return rc;
-      if ((rc = linear(l.wv, b.h, b.qkv + qd + kvd, l.bv, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = norm_linear(l.wq, b.x, l.attn_norm, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK)
+        return rc;
+      if ((rc = norm_linear(l.wk, b.x, l.attn_norm, b.qkv + qd, l.bk, MLQ_EPI_NONE)) != MLQ_OK)
+        return rc;
+      if ((rc = norm_linear(l.wv, b.x, l.attn_norm, b.qkv + qd + kvd, l.bv, MLQ_EPI_NONE)) !=
+          MLQ_OK)
+        return rc;
     }
     RopeLaunch r;
     r.q = b.qkv;
@@ -356,13 +376,16 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     // x2 = x + wo . attn: the residual enters as the projection's bias
     if ((rc = linear(l.wo, b.attn, b.x2, b.x, MLQ_EPI_NONE)) != MLQ_OK) return rc;
     // FFN sublayer
-    if ((rc = hip(launch_rmsnorm(b.x2, l.ffn_norm, b.h, 1, dim, m->rms_norm_eps, s))) != MLQ_OK)
-      return rc;
     if (glu_fused(l)) {
-      if ((rc = linear(l.w_gate, b.h, b.ffn, nullptr, MLQ_EPI_SWIGLU)) != MLQ_OK) return rc;
+      if ((rc = norm_linear(l.w_gate, b.x2, l.ffn_norm, b.ffn, nullptr, MLQ_EPI_SWIGLU)) !=
+          MLQ_OK)
+        return rc;
     } else {
-      if ((rc = linear(l.w_gate, b.h, b.gate, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
-      if ((rc = linear(l.w_up, b.h, b.up, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = norm_linear(l.w_gate, b.x2, l.ffn_norm, b.gate, nullptr, MLQ_EPI_NONE)) !=
+          MLQ_OK)
+        return rc;
+      if ((rc = norm_linear(l.w_up, b.x2, l.ffn_norm, b.up, nullptr, MLQ_EPI_NONE)) != MLQ_OK)
+        return rc;
       if ((rc = hip(launch_eltwise(kEltSwiGLU, b.gate, b.up, b.ffn, m->hidden_dim, s))) != MLQ_OK)
         return rc;
     }
@@ -370,9 +393,7 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     if ((rc = linear(l.w_down, b.ffn, b.x, b.x2, MLQ_EPI_NONE)) != MLQ_OK) return rc;
   }
   // computeLogitsDevice (src/forward.cc:736-745)
-  if ((rc = hip(launch_rmsnorm(b.x, m->final_norm, b.h, 1, dim, m->rms_norm_eps, s))) != MLQ_OK)
-    return rc;
-  return linear(m->lm_head, b.h, logits, nullptr, MLQ_EPI_NONE);
+  return norm_linear(m->lm_head, b.x, m->final_norm, logits, nullptr, MLQ_EPI_NONE);
 }
 
 }  // extern "C"

@@ -17,17 +17,6 @@
 namespace mlq {
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  return v;
-}
-
 // Reductions over the first N lanes of each 16-lane row with DPP (VALU
 // lane permutes, no LDS round trip): xor 1 and xor 2 as quad permutes, then
 // row_half_mirror (lane i <-> 7 - i: pairs the two quads of 8 lanes) and

@@ -121,6 +121,18 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   return as_u32(h);
 }
 
+// Sum / max over the 64 lanes of a wave (every lane gets the result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
 // ---- output epilogue (Epilogue, kEpi* in launch.h) ---------------------------
 // silu in fp32 with the hardware exp (v_exp_f32 on g * log2(e)): within a
 // few ulp of g / (1 + expf(-g))

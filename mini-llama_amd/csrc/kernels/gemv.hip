@@ -186,7 +186,7 @@ __device__ __forceinline__ float block_sum8(float v) {
   return v;
 }
 
-template <int QT, int MR, int GW, bool RING>
+template <int QT, int MR, int GW, bool RING, bool NORM>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int M = a.m;
@@ -230,7 +230,13 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // covers one float4 per lane of every row (2 groups). The rest, if any,
   // is staged after the weight loads are issued.
   constexpr int XR = MR == 1 ? kXRegs : kGemvMaxRows;
-  float4 xr[XR];
+  // Input RMSNorm (one row): the norm weight is loaded beside x, the staged
+  // values are x * weight and the lanes keep sum(x^2) of their elements.
+  // (its register-held part is loaded with x: reading it at staging time
+  // instead delays the first MFMA by a round trip, measured slower)
+  constexpr bool norm = NORM && MR == 1;
+  const rsrc_t rg = make_rsrc(norm ? a.epi.norm + kbase : a.x, norm ? xbytes : 0u);
+  float4 xr[XR], gr[norm ? XR : 1];
 #pragma unroll
   for (int i = 0; i < XR; ++i) {
     const int r = MR == 1 ? 0 : i;
@@ -238,8 +244,17 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     if (r < M && (MR > 1 || 64 * i < c4)) {  // wave-uniform
       const rsrc_t rx = make_rsrc(a.x + (size_t)r * a.k + kbase, xbytes);
       xr[i] = load_x4(rx, c < c4 ? c : 0x2000000, vec);
+      if constexpr (norm) gr[i] = load_x4(rg, c < c4 ? c : 0x2000000, vec);
     }
   }
+  float ssq = 0.0f;  // this lane's sum of x^2 (norm only)
+  auto normed = [&](float4 v, float4 g) {
+    ssq += v.x * v.x;
+    ssq += v.y * v.y;
+    ssq += v.z * v.z;
+    ssq += v.w * v.w;
+    return float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
+  };
 
   // ---- weight loads: the first GW groups of the slice --------------------
   // Issued group by group (not clustered by kind), so group 0 can start as
@@ -259,7 +274,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     const int c = MR == 1 ? lane + 64 * i : lane;
     if (r < M && (MR > 1 || 64 * i < c4)) {  // wave-uniform
       float sx = 0.0f;
-      if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, xr[i]);
+      float4 v = xr[i];
+      if constexpr (norm) v = normed(v, gr[i]);
+      if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, v);
       if (QT == MLQ_Q4_1) {
         sx = block_sum8(sx);
         if (c < c4 && (c & 7) == 0) xsum[r * nblk + (c >> 3)] = sx;
@@ -275,7 +292,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       for (int cb = c_done; cb < c4; cb += 64) {
         const int c = cb + lane;
         float sx = 0.0f;
-        if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, load_x4(rx, c, vec));
+        float4 v = load_x4(rx, c, vec);
+        if constexpr (norm) v = normed(v, load_x4(rg, c, vec));
+        if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, v);
         if (QT == MLQ_Q4_1) {
           sx = block_sum8(sx);
           if (c < c4 && (c & 7) == 0) xsum[r * nblk + (c >> 3)] = sx;
@@ -362,8 +381,19 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   }
 
   // ---- output ------------------------------------------------------------
+  // RMSNorm scale of the (single) row: sum(x^2) over lanes, then over the
+  // K slices of the workgroup in slice order
+  float nscale = 1.0f;
+  if constexpr (norm) {
+    ssq = wave_sum(ssq);
+    if (a.split == 1) nscale = sqrtf(ssq / (float)a.k + a.epi.norm_eps);
+  }
   if (a.split == 1) {
     const int row = tile * kTileRows + n;
+    if (norm) {
+      acc0 = acc0 / nscale;
+      acc1 = acc1 / nscale;
+    }
     const float v0 = add_bias(a.epi, acc0, min(row, a.n - 1));
     const float v1 = add_bias(a.epi, acc1, min(row, a.n - 1));
     if (a.epi.act == kEpiSwiGLU) {
@@ -385,11 +415,18 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // K slices combine in slice order (deterministic)
   if (r0 < M) part[(wave * M + r0) * kTileRows + n] = acc0;
   if (MR > 1 && r1 < M) part[(wave * M + r1) * kTileRows + n] = acc1;
+  float* ssp = part + (size_t)a.split * M * kTileRows;  // per-slice sum(x^2)
+  if (norm && lane == 0) ssp[wave] = ssq;
   __syncthreads();
+  if constexpr (norm) {
+    float t = 0.0f;
+    for (int w = 0; w < a.split; ++w) t += ssp[w];
+    nscale = sqrtf(t / (float)a.k + a.epi.norm_eps);
+  }
   auto slice_sum = [&](int r, int nn) {
     float s = 0.0f;
     for (int w = 0; w < a.split; ++w) s += part[(w * M + r) * kTileRows + nn];
-    return s;
+    return norm ? s / nscale : s;
   };
   if (a.epi.act == kEpiSwiGLU) {
     for (int o = tid; o < M * 8; o += blockDim.x) {
@@ -502,14 +539,14 @@ Plan make_plan(int type, int m, const Geometry& geo) {
     p.gw = (geo.g + split - 1) / split;
     p.wave_lds = wave_lds_bytes(type, m, p.gw);
     p.lds = p.wave_lds * split +
-            (split > 1 ? (size_t)split * m * kTileRows * 4 : 0);
+            (split > 1 ? (size_t)split * (m * kTileRows + 1) * 4 : 0);
     if (p.lds <= lds_limit() || split >= kMaxSplit) break;
     split *= 2;
   }
   // every wave of the workgroup must own at least one group
   p.split = (geo.g + p.gw - 1) / p.gw;
   p.lds = p.wave_lds * p.split +
-          (p.split > 1 ? (size_t)p.split * m * kTileRows * 4 : 0);
+          (p.split > 1 ? (size_t)p.split * (m * kTileRows + 1) * 4 : 0);
   // Every group of the slice in flight at once (depth = gw) when it fits,
   // otherwise the ring.
   p.ring = p.gw > max_depth(type, m);
@@ -518,19 +555,36 @@ Plan make_plan(int type, int m, const Geometry& geo) {
   return p;
 }
 
-template <int QT, int MR, int GW, bool RING>
-hipError_t launch_typed(const GemvArgs& a, size_t lds, hipStream_t stream) {
+template <int QT, int MR, int GW, bool RING, bool NORM>
+hipError_t launch_kernel(const GemvArgs& a, size_t lds, hipStream_t stream) {
   // Opt in to more than the default 64 KiB of dynamic LDS when needed.
   static size_t configured = 64 * 1024;
   if (lds > configured) {
     hipError_t e = hipFuncSetAttribute(
-        (const void*)gemv_kernel<QT, MR, GW, RING>,
+        (const void*)gemv_kernel<QT, MR, GW, RING, NORM>,
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     configured = lds;
   }
-  gemv_kernel<QT, MR, GW, RING><<<a.nt, 64 * a.split, lds, stream>>>(a);
+  gemv_kernel<QT, MR, GW, RING, NORM><<<a.nt, 64 * a.split, lds, stream>>>(a);
   return hipGetLastError();
+}
+
+// The input-RMSNorm variant exists for one activation row, and not for the
+// deepest non-ring slices (q8_0 depth 9-10, q4_1 depth 6), whose register
+// budget the norm weight's registers would overflow.
+constexpr bool norm_variant(int qt, int gw, bool ring) {
+  return ring || !((qt == MLQ_Q8_0 && gw >= 9) || (qt == MLQ_Q4_1 && gw >= 6));
+}
+
+template <int QT, int MR, int GW, bool RING>
+hipError_t launch_typed(const GemvArgs& a, size_t lds, hipStream_t stream) {
+  if (a.epi.norm != nullptr) {
+    if constexpr (MR == 1 && norm_variant(QT, GW, RING))
+      return launch_kernel<QT, MR, GW, RING, true>(a, lds, stream);
+    return hipErrorInvalidValue;
+  }
+  return launch_kernel<QT, MR, GW, RING, false>(a, lds, stream);
 }
 
 template <int QT, int MR>
@@ -581,6 +635,16 @@ hipError_t launch_rows(const GemvArgs& a, const Plan& p, hipStream_t stream) {
 
 void set_gemv_split(int split) { g_split_override = split; }
 
+bool gemv_norm_supported(const mlq_weight& w) {
+  if (w.type != MLQ_Q8_0 && w.type != MLQ_Q4_0 && w.type != MLQ_Q4_1) return false;
+  const Plan p = make_plan(w.type, 1, geometry(w.n, w.k));
+  if (p.lds > lds_limit()) return false;
+  // the variant launch_depth would pick for this plan
+  int depth = p.depth;
+  if (!p.ring && w.type == MLQ_Q4_1) depth = std::min(depth, 6);
+  return norm_variant(w.type, depth, p.ring);
+}
+
 int gemv_max_k(int type, int m) {
   if (m < 1 || m > kGemvMaxRows) return 0;
   // the largest K whose default plan fits the LDS budget
@@ -597,6 +661,7 @@ hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream, const Epilogue& epi) {
   const Geometry geo = geometry(w.n, w.k);
   if (m < 1 || m > kGemvMaxRows) return hipErrorInvalidValue;
+  if (epi.norm != nullptr && m != 1) return hipErrorInvalidValue;
   const Plan p = make_plan(w.type, m, geo);
   if (p.lds > lds_limit()) return hipErrorInvalidValue;
   GemvArgs a;

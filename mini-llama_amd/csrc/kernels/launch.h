@@ -21,6 +21,12 @@ enum { kEpiNone = 0, kEpiSwiGLU = 1 };
 struct Epilogue {
   const float* bias = nullptr;  // [n] or nullptr
   int act = kEpiNone;
+  // Input RMSNorm (decode GEMV with one activation row only): with norm
+  // non-null the kernel computes W . (x * norm) / sqrt(mean(x^2) + norm_eps)
+  // in place of W . x, i.e. the Linear of rmsNorm(x, norm, eps)
+  // (src/ops.cc:43-72) without a separate pass over x.
+  const float* norm = nullptr;  // [k] or nullptr
+  float norm_eps = 0.0f;
 };
 
 // capi.cpp: MLQ status of a HIP result, recorded for mlq_last_hip_error.
@@ -41,6 +47,9 @@ hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream, const Epilogue& epi = Epilogue());
 // Largest k the GEMV accepts for m rows (LDS-bound).
 int gemv_max_k(int type, int m);
+// epi.norm is honoured by the decode GEMV with m == 1 for the weights this
+// accepts (launch_gemv returns hipErrorInvalidValue for the others).
+bool gemv_norm_supported(const mlq_weight& w);
 // Split override (0 = automatic); validated by the caller.
 void set_gemv_split(int split);
 

@@ -29,12 +29,6 @@ struct F32Args {
   Epilogue epi;
 };
 
-__device__ __forceinline__ float wave_sum32(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
 template <int MR, bool VEC>
 __global__ __launch_bounds__(256) void linear_f32_kernel(F32Args a) {
   const int wave = threadIdx.x >> 6;
@@ -88,7 +82,7 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(F32Args a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int r = 0; r < MR; ++r) acc[i][r] = wave_sum32(acc[i][r]);
+    for (int r = 0; r < MR; ++r) acc[i][r] = wave_sum(acc[i][r]);
   if (lane != 0) return;
 #pragma unroll
   for (int r = 0; r < MR; ++r) {
