@@ -48,6 +48,7 @@ struct DecodeBuffers {
   float* gate;  // unfused gate / up outputs [hidden] each
   float* up;
   float* apart; // attention partials
+  float* rope;  // the step's RoPE table: cos then sin of each pair's angle
   void* lin;    // Linear workspace
   size_t lin_bytes;
   size_t total;
@@ -122,6 +123,7 @@ int plan(const mlq_model* m, char* base, DecodeBuffers* b) {
   b->ffn = take(hid);
   b->gate = take(hid);
   b->up = take(hid);
+  b->rope = take(m->head_dim);
   b->apart = (float*)(base ? base + off : nullptr);
   off += align256(attention_workspace_bytes(m->n_heads, m->head_dim, m->max_seq_len));
   b->lin = base ? base + off : nullptr;
@@ -324,8 +326,21 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     return linear(w, b.h, y, bias, act);
   };
 
+  // RoPE and the cache write ride in the attention kernel where it can take
+  // them (register kernel: head_dim 64 / 128 / 256, 16-byte aligned cache);
+  // the embedding launch then also writes the step's RoPE table.
+  const bool fused_rope = attention_fusable(hd, m->n_heads / m->n_kv_heads) &&
+                          ((uintptr_t)c->keys & 15) == 0 && ((uintptr_t)c->values & 15) == 0;
+  RopeTable rt;
+  if (fused_rope) {
+    rt.cs = b.rope;
+    rt.pos_dev = pos_dev;
+    rt.pos = pos;
+    rt.hd = hd;
+    rt.theta = m->rope_theta;
+  }
   if ((rc = hip(launch_embedding(m->token_embedding, m->vocab_size, dim, token_dev, token,
-                                 b.x, s))) != MLQ_OK)
+                                 b.x, s, rt))) != MLQ_OK)
     return rc;
   for (int li = 0; li < m->n_layers; ++li) {
     const mlq_layer& l = m->layers[li];
@@ -342,22 +357,24 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
           MLQ_OK)
         return rc;
     }
-    RopeLaunch r;
-    r.q = b.qkv;
-    r.k = b.qkv + qd;
-    r.v = b.qkv + qd + kvd;
-    r.keys = c->keys;
-    r.values = c->values;
-    r.n_heads = m->n_heads;
-    r.n_kv = m->n_kv_heads;
-    r.hd = hd;
-    r.neox = m->rope_type == MLQ_ROPE_NEOX;
-    r.layer = li;
-    r.max_seq = c->max_seq_len;
-    r.pos_dev = pos_dev;
-    r.pos = pos;
-    r.theta = m->rope_theta;
-    if ((rc = hip(launch_rope(r, s))) != MLQ_OK) return rc;
+    if (!fused_rope) {
+      RopeLaunch r;
+      r.q = b.qkv;
+      r.k = b.qkv + qd;
+      r.v = b.qkv + qd + kvd;
+      r.keys = c->keys;
+      r.values = c->values;
+      r.n_heads = m->n_heads;
+      r.n_kv = m->n_kv_heads;
+      r.hd = hd;
+      r.neox = m->rope_type == MLQ_ROPE_NEOX;
+      r.layer = li;
+      r.max_seq = c->max_seq_len;
+      r.pos_dev = pos_dev;
+      r.pos = pos;
+      r.theta = m->rope_theta;
+      if ((rc = hip(launch_rope(r, s))) != MLQ_OK) return rc;
+    }
     AttnLaunch a;
     a.q = b.qkv;
     a.keys = c->keys;
@@ -372,6 +389,12 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     a.max_len = pos_dev != nullptr ? m->max_seq_len : pos + 1;
     a.pos_dev = pos_dev;
     a.pos = pos;
+    if (fused_rope) {
+      a.k_new = b.qkv + qd;
+      a.v_new = b.qkv + qd + kvd;
+      a.rope_cs = b.rope;
+      a.neox = m->rope_type == MLQ_ROPE_NEOX;
+    }
     if ((rc = hip(launch_attention(a, s))) != MLQ_OK) return rc;
     // x2 = x + wo . attn: the residual enters as the projection's bias
     if ((rc = linear(l.wo, b.attn, b.x2, b.x, MLQ_EPI_NONE)) != MLQ_OK) return rc;

@@ -144,14 +144,31 @@ __global__ __launch_bounds__(256) void eltwise_kernel(const float* __restrict__ 
 // ---- embedding ------------------------------------------------------------------
 // y = table[token] (embeddingLookupKernel, src/cuda_ops.cu:415-421). A device
 // token outside [0, vocab) yields a NaN row instead of a wild read.
+// With rope_cs non-null, workgroup 0 also writes the step's RoPE table for
+// position pos: rope_cs[i] = cos(pos * f_i), rope_cs[hd/2 + i] = sin(pos * f_i)
+// with f_i = 1 / theta^(2i/hd), the angle of pair i in both pairings
+// (src/ops.cc:146-151, 168-173), shared by every layer of the step.
 __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ table,
                                                     int vocab, int dim,
                                                     const int32_t* token_dev, int token,
-                                                    float* __restrict__ y) {
+                                                    float* __restrict__ y, float* rope_cs,
+                                                    const int32_t* pos_dev, int pos, int hd,
+                                                    float theta) {
   const int t = read_scalar(token_dev, token);
   const bool ok = t >= 0 && t < vocab;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x)
     y[i] = ok ? table[(size_t)t * dim + i] : __builtin_nanf("");
+  if (rope_cs != nullptr && blockIdx.x == 0) {
+    const int p = read_scalar(pos_dev, pos);
+    const int half = hd >> 1;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+      const float freq = 1.0f / powf(theta, (float)(2 * i) / (float)hd);
+      float sn, cs;
+      sincosf((float)p * freq, &sn, &cs);
+      rope_cs[i] = cs;
+      rope_cs[half + i] = sn;
+    }
+  }
 }
 
 // ---- RoPE + KV-cache write ---------------------------------------------------------
@@ -264,6 +281,17 @@ struct AttnArgs {
   const int32_t* pos_dev;
   int pos;
   float scale;
+  // Fused RoPE + cache write (register kernel only): q is the raw projection,
+  // k_new / v_new the raw k and v of position pos ([n_kv][hd]), rope_cs the
+  // step's table; the workgroup holding pos writes its rotated k and its v
+  // to cache row (layer, pos) and every read of that row takes the raw
+  // values instead.
+  const float* k_new;
+  const float* v_new;
+  const float* rope_cs;
+  float* kc;             // the cache, writable (same arrays as keys / values)
+  float* vc;
+  int neox;
 };
 
 template <int HD, int GMAX>
@@ -391,7 +419,20 @@ __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
   }
 }
 
-template <int HD, int GMAX>
+// One rotated element of a head: element d of x (raw), its RoPE partner
+// (d ^ 1 normal, d +- hd/2 NeoX) and the step's table.
+template <int HD>
+__device__ __forceinline__ float rope_elem(const float* x, int d, int neox, const float* cs) {
+  constexpr int H = HD / 2;
+  const int i = neox ? (d < H ? d : d - H) : (d >> 1);
+  const bool first = neox ? d < H : (d & 1) == 0;
+  const float c = cs[i], sn = cs[H + i];
+  const float x0 = first ? x[d] : x[neox ? d - H : d - 1];
+  const float x1 = first ? x[neox ? d + H : d + 1] : x[d];
+  return first ? x0 * c - x1 * sn : x0 * sn + x1 * c;
+}
+
+template <int HD, int GMAX, bool FUSED>
 __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a) {
   constexpr int KD = 32;          // dims of K per lane
   constexpr int L = HD / KD;      // lanes per position
@@ -427,17 +468,50 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
 #pragma unroll
   for (int i = 0; i < KF; ++i) kreg[i] = kr[i];
   float vreg[P][VJ];
+  const float* vnew = FUSED ? a.v_new + (size_t)kvh * HD : nullptr;
 #pragma unroll
-  for (int t = 0; t < P; ++t)
+  for (int t = 0; t < P; ++t) {
+    // (fused: the current position's row is not in the cache yet; rows past
+    // it only feed weights of zero and read the current row too)
+    const float* vrow = FUSED && t0 + t >= pos ? vnew
+                                               : a.values + base + (size_t)min(t, last) * row_stride;
 #pragma unroll
-    for (int j = 0; j < VJ; ++j)
-      vreg[t][j] = a.values[base + (size_t)min(t, last) * row_stride + j * 64 + lane];
+    for (int j = 0; j < VJ; ++j) vreg[t][j] = vrow[j * 64 + lane];
+  }
   // q of the group's heads; heads G..GMAX-1 are zero so every head loop
   // below runs a fixed GMAX times with no per-head branches (their results
   // are never stored), which lets the heads' reductions interleave
-  const f4_t* q4 = (const f4_t*)(a.q + (size_t)kvh * G * HD);
-  for (int i = threadIdx.x; i < GMAX * HD / 4; i += W * 64)
-    qs[i] = i < G * HD / 4 ? q4[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (FUSED) {
+    const float* qraw = a.q + (size_t)kvh * G * HD;
+    float* qf = (float*)qs;
+    for (int i = threadIdx.x; i < GMAX * HD; i += W * 64) {
+      const int g = i / HD;
+      qf[i] = g < G ? rope_elem<HD>(qraw + (size_t)g * HD, i - g * HD, a.neox, a.rope_cs) : 0.0f;
+    }
+    if (t0 + tp == pos) {  // this lane's piece of the current key, rotated
+      const float* kraw = a.k_new + (size_t)kvh * HD;
+#pragma unroll
+      for (int i = 0; i < KF; ++i) {
+        const int d = part * KD + 4 * i;
+        kreg[i] = f4_t{rope_elem<HD>(kraw, d, a.neox, a.rope_cs),
+                       rope_elem<HD>(kraw, d + 1, a.neox, a.rope_cs),
+                       rope_elem<HD>(kraw, d + 2, a.neox, a.rope_cs),
+                       rope_elem<HD>(kraw, d + 3, a.neox, a.rope_cs)};
+      }
+    }
+    if (tb + W * P > pos) {  // the workgroup holding pos: write the cache row
+      const int d = threadIdx.x;
+      const size_t row = (((size_t)a.layer * a.max_seq + pos) * a.n_kv + kvh) * HD;
+      if (d < HD) {
+        a.kc[row + d] = rope_elem<HD>(a.k_new + (size_t)kvh * HD, d, a.neox, a.rope_cs);
+        a.vc[row + d] = vnew[d];
+      }
+    }
+  } else {
+    const f4_t* q4 = (const f4_t*)(a.q + (size_t)kvh * G * HD);
+    for (int i = threadIdx.x; i < GMAX * HD / 4; i += W * 64)
+      qs[i] = i < G * HD / 4 ? q4[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  }
   __syncthreads();
 
   // scores: this lane's KD dims, then the L parts summed across lanes
@@ -762,10 +836,10 @@ hipError_t launch_eltwise(int op, const float* a, const float* b, float* y, int6
 }
 
 hipError_t launch_embedding(const float* table, int vocab, int dim, const int32_t* token_dev,
-                            int token, float* y, hipStream_t stream) {
+                            int token, float* y, hipStream_t stream, const RopeTable& rt) {
   const int blocks = (dim + 255) / 256;
   hipLaunchKernelGGL(embed_kernel, dim3(blocks), dim3(256), 0, stream, table, vocab, dim,
-                     token_dev, token, y);
+                     token_dev, token, y, rt.cs, rt.pos_dev, rt.pos, rt.hd, rt.theta);
   return hipGetLastError();
 }
 
@@ -809,6 +883,13 @@ size_t attention_workspace_bytes(int n_heads, int hd, int max_len) {
   return ((size_t)n_heads * c * (2 + (size_t)hd)) * sizeof(float);
 }
 
+// The register kernel (and so the fused RoPE + cache write) covers head
+// dims 64 / 128 / 256, except head_dim 64 with more than 8 query heads per
+// kv head, which would spill.
+bool attention_fusable(int hd, int group) {
+  return attn_reg_hd(hd) && !(hd == 64 && group > 8);
+}
+
 bool attention_supported(int n_heads, int n_kv, int hd) {
   return n_kv > 0 && n_heads % n_kv == 0 && n_heads / n_kv <= kAttnMaxGroup && hd > 0 &&
          hd <= kAttnMaxHd;
@@ -817,8 +898,12 @@ bool attention_supported(int n_heads, int n_kv, int hd) {
 template <int HD, int GMAX>
 static void attn_launch(const AttnArgs& a, hipStream_t stream) {
   if constexpr (HD != 0) {
-    hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX>), dim3(a.chunks, a.n_kv),
-                       dim3(kAttnRegWaves * 64), 0, stream, a);
+    if (a.rope_cs != nullptr)
+      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, true>), dim3(a.chunks, a.n_kv),
+                         dim3(kAttnRegWaves * 64), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, false>), dim3(a.chunks, a.n_kv),
+                         dim3(kAttnRegWaves * 64), 0, stream, a);
   } else {
     constexpr int CH = kAttnLdsChunk;
     const int hdp = (a.hd + 3) & ~3;
@@ -852,8 +937,14 @@ hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   a.vec = r.hd % 4 == 0 && ((uintptr_t)r.keys & 15) == 0 && ((uintptr_t)r.values & 15) == 0;
   // (head_dim 64 with more than 8 query heads per kv head would spill the
   // register kernel: it takes the LDS kernel)
-  const bool reg = attn_reg_hd(r.hd) && a.vec && ((uintptr_t)r.q & 15) == 0 &&
-                   !(r.hd == 64 && a.group > 8);
+  const bool reg = attention_fusable(r.hd, a.group) && a.vec && ((uintptr_t)r.q & 15) == 0;
+  a.k_new = r.k_new;
+  a.v_new = r.v_new;
+  a.rope_cs = r.rope_cs;
+  a.kc = const_cast<float*>(r.keys);
+  a.vc = const_cast<float*>(r.values);
+  a.neox = r.neox;
+  if (r.rope_cs != nullptr && !reg) return hipErrorInvalidValue;
   a.chunk_len = reg ? attn_reg_chunk(r.hd) : kAttnLdsChunk;
   a.chunks = (r.max_len + a.chunk_len - 1) / a.chunk_len;
   a.pos_dev = r.pos_dev;

@@ -92,9 +92,18 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, in
 enum { kEltAdd = 0, kEltMul = 1, kEltSilu = 2, kEltSwiGLU = 3 };
 hipError_t launch_eltwise(int op, const float* a, const float* b, float* y, int64_t n,
                           hipStream_t stream);
-// token_dev (device int32, may be null) overrides token.
+// token_dev (device int32, may be null) overrides token. With rt.cs
+// non-null the launch also writes the step's RoPE table (cos of pair i at
+// cs[i], sin at cs[hd/2 + i]) for position pos (pos_dev overrides).
+struct RopeTable {
+  float* cs = nullptr;
+  const int32_t* pos_dev = nullptr;
+  int pos = 0, hd = 0;
+  float theta = 10000.0f;
+};
 hipError_t launch_embedding(const float* table, int vocab, int dim, const int32_t* token_dev,
-                            int token, float* y, hipStream_t stream);
+                            int token, float* y, hipStream_t stream,
+                            const RopeTable& rt = RopeTable());
 // RoPE on q [n_heads][hd] and k [n_kv][hd] at position pos (pos_dev
 // overrides). With keys/values non-null the rotated k and v go to cache row
 // (layer, pos) of a [layers][max_seq][n_kv][hd] cache and k is left as is.
@@ -126,8 +135,18 @@ struct AttnLaunch {
   int max_len = 0;
   const int32_t* pos_dev = nullptr;
   int pos = 0;
+  // Fused RoPE + cache write of position pos (attention_fusable shapes):
+  // q is then the raw projection, k_new / v_new the raw k and v [n_kv][hd],
+  // rope_cs the step's table (launch_embedding), and the cache row (layer,
+  // pos) is written here. rope_cs == nullptr: q is rotated and the row is
+  // in the cache already.
+  const float* k_new = nullptr;
+  const float* v_new = nullptr;
+  const float* rope_cs = nullptr;
+  int neox = 0;
 };
 bool attention_supported(int n_heads, int n_kv, int hd);
+bool attention_fusable(int hd, int group);
 int attention_chunks(int hd, int max_len);
 size_t attention_workspace_bytes(int n_heads, int hd, int max_len);
 hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream);
