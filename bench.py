@@ -283,7 +283,7 @@ def decode_bytes(dm, pos):
     return dm.weight_bytes + kv + 4 * c["dim"] + 4 * c["vocab_size"]
 
 
-def bench_decode(pkg, torch, steps, warmup, context=1024, qtype="q4_0"):
+def bench_decode(pkg, torch, steps, warmup, context=1024, qtype="q4_0", prefill_tokens=512):
     """Whole decode steps of a Qwen2-7B-shaped q4_0 model (28 layers, q|k|v
     biases, NeoX rope, random weights) at positions context..context+steps-1:
     eager mlq_decode_token calls, then one HIP graph of step + greedy
@@ -326,14 +326,42 @@ def bench_decode(pkg, torch, steps, warmup, context=1024, qtype="q4_0"):
     assert np.isfinite(dm.logits.cpu().numpy()).all()
     nbytes = decode_bytes(dm, context + steps // 2)
     gbs = nbytes / (graph_ms * 1e-3) / 1e9
-    return {"workload": f"Qwen2-7B-shaped {qtype} decode step (28 layers, dim 3584, FFN 18944, "
-                        "28/4 heads, head_dim 128, vocab 152064, q|k|v bias), "
-                        f"positions {context}..{context + steps - 1}",
-            "tokens_per_s": 1e3 / graph_ms, "ms_per_token": graph_ms,
-            "ms_per_token_eager": eager_ms, "bytes_per_token": nbytes,
-            "weight_bytes": dm.weight_bytes, "gbs": gbs, "steps": steps,
-            "roofline_tokens_per_s": HBM_PEAK_GBS * 1e9 / nbytes,
-            "frac_hbm": gbs / HBM_PEAK_GBS}
+    out = {"workload": f"Qwen2-7B-shaped {qtype} decode step (28 layers, dim 3584, FFN 18944, "
+                       "28/4 heads, head_dim 128, vocab 152064, q|k|v bias), "
+                       f"positions {context}..{context + steps - 1}",
+           "tokens_per_s": 1e3 / graph_ms, "ms_per_token": graph_ms,
+           "ms_per_token_eager": eager_ms, "bytes_per_token": nbytes,
+           "weight_bytes": dm.weight_bytes, "gbs": gbs, "steps": steps,
+           "roofline_tokens_per_s": HBM_PEAK_GBS * 1e9 / nbytes,
+           "frac_hbm": gbs / HBM_PEAK_GBS}
+    if prefill_tokens:
+        out["prefill"] = bench_prefill(dm, torch, prefill_tokens, max(2, steps // 25))
+    return out
+
+
+def bench_prefill(dm, torch, n, reps):
+    """mlq_prefill of an n-token prompt at position 0 (every Linear on
+    [n, K]), repeated; tokens/s and the Linear FLOP rate (2 * n * the
+    parameters of every layer's projections, lm_head for the last row)."""
+    c = dm.config
+    rng = np.random.default_rng(3)
+    toks = rng.integers(0, c["vocab_size"], n).tolist()
+    log(f"prefill: {n} tokens x {reps}")
+    dm.prefill(toks, 0)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dm.prefill(toks, 0)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    hd, dim, hid = c["head_dim"], c["dim"], c["hidden_dim"]
+    layer = dim * (c["n_heads"] + 2 * c["n_kv_heads"]) * hd + c["n_heads"] * hd * dim + 3 * dim * hid
+    flops = 2.0 * n * layer * c["n_layers"] + 2.0 * c["vocab_size"] * dim
+    return {"tokens": n, "ms": ms, "tokens_per_s": n / (ms * 1e-3),
+            "linear_tflops": flops / (ms * 1e-3) / 1e12, "reps": reps}
 
 
 def cpu_baseline(qtype, n, k, budget_s=10.0):

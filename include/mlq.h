@@ -379,6 +379,19 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
                      const int32_t* token_dev, const int32_t* pos_dev, float* logits,
                      void* ws, size_t ws_bytes, mlq_stream_t stream);
 
+/* Batched prefill: the n_tokens tokens (host array) at positions start_pos
+ * .. start_pos + n_tokens - 1 through the model at once, every Linear on
+ * [n_tokens, K] activations (the skinny and prefill GEMMs), their K/V rows
+ * written to the cache, and logits [vocab_size] (device) of the last token:
+ * the result of forwardBatch (src/batch.cc:32-55), which runs forwardToken
+ * once per token. Attention is causal (row r sees positions up to
+ * start_pos + r). Tokens out of range or start_pos + n_tokens beyond
+ * max_seq_len are MLQ_ERR_INVALID_ARG. ws: mlq_prefill_workspace(m,
+ * n_tokens) bytes, 256-byte aligned. */
+int mlq_prefill_workspace(const mlq_model* m, int n_tokens, size_t* bytes);
+int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens, int n_tokens,
+                int start_pos, float* logits, void* ws, size_t ws_bytes, mlq_stream_t stream);
+
 /* Greedy sampling on the device (argMax, src/ops.cc:230-246, as the
  * sampler's temperature-0 choice, MiniSampler::sampleGreedy,
  * src/sampler.cc:109-114): *token_dev = argmax(logits), then *pos_dev += 1,

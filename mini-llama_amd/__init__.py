@@ -154,6 +154,8 @@ SIGNATURES = {
     "mlq_argmax": ([_P, _I64, _P, _P], _I),
     "mlq_decode_workspace": ([_MP, ctypes.POINTER(_Z)], _I),
     "mlq_decode_token": ([_MP, _KVP, _I, _I, _P, _P, _P, _P, _Z, _P], _I),
+    "mlq_prefill_workspace": ([_MP, _I, ctypes.POINTER(_Z)], _I),
+    "mlq_prefill": ([_MP, _KVP, _P, _I, _I, _P, _P, _Z, _P], _I),
     "mlq_argmax_workspace": ([_I64, ctypes.POINTER(_Z)], _I),
     "mlq_greedy_next": ([_P, _I, _P, _P, _P, _Z, _P], _I),
 }

@@ -5,6 +5,7 @@
 // return codes; every launch is stream-ordered and nothing synchronizes.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 
@@ -129,6 +130,81 @@ int plan(const mlq_model* m, char* base, DecodeBuffers* b) {
   b->lin = base ? base + off : nullptr;
   b->lin_bytes = lin;
   off += align256(lin);
+  b->total = off;
+  return MLQ_OK;
+}
+
+// ---- prefill (forwardBatch over [n, K] Linears) -------------------------------
+// Query rows per attention launch: bounds the partial workspace.
+constexpr int kPrefillAttnRows = 64;
+
+struct PrefillBuffers {
+  int32_t* tokens;  // [n]
+  float* x;         // residual stream [n][dim]
+  float* x2;        // after attention [n][dim]
+  float* h;         // normalised activations / projection output [n][dim]
+  float* qkv;       // [n][qd + 2 kvd] (fused) or q [n][qd]
+  float* k;         // unfused: [n][kvd] each
+  float* v;
+  float* attn;      // [n][qd]
+  float* ffn;       // [n][hidden]
+  float* gate;      // unfused: [n][hidden] each
+  float* up;
+  float* apart;     // attention partials for kPrefillAttnRows rows
+  void* lin;        // Linear workspace for n rows (and 1 row)
+  size_t lin_bytes;
+  size_t total;
+};
+
+int plan_prefill(const mlq_model* m, int n, char* base, PrefillBuffers* b) {
+  DecodeBuffers d;
+  int rc = plan(m, nullptr, &d);  // model checks
+  if (rc != MLQ_OK) return rc;
+  if (n <= 0) return MLQ_ERR_SHAPE;
+  const int dim = m->dim, hid = m->hidden_dim;
+  const int qd = m->n_heads * m->head_dim, kvd = m->n_kv_heads * m->head_dim;
+  bool any_unfused_qkv = false, any_unfused_glu = false;
+  size_t lin = d.lin_bytes;
+  auto need = [&](const mlq_weight& w) {
+    size_t bytes = 0;
+    if (mlq_linear_workspace(&w, n, &bytes) == MLQ_OK && bytes > lin) lin = bytes;
+  };
+  for (int i = 0; i < m->n_layers; ++i) {
+    const mlq_layer& l = m->layers[i];
+    any_unfused_qkv |= !qkv_fused(l);
+    any_unfused_glu |= !glu_fused(l);
+    need(l.wq);
+    if (!qkv_fused(l)) {
+      need(l.wk);
+      need(l.wv);
+    }
+    need(l.wo);
+    need(l.w_gate);
+    if (!glu_fused(l)) need(l.w_up);
+    need(l.w_down);
+  }
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  const size_t f = sizeof(float), rows = (size_t)n;
+  b->tokens = (int32_t*)take(rows * sizeof(int32_t));
+  b->x = (float*)take(rows * dim * f);
+  b->x2 = (float*)take(rows * dim * f);
+  b->h = (float*)take(rows * dim * f);
+  b->qkv = (float*)take(rows * (qd + 2 * kvd) * f);
+  b->k = any_unfused_qkv ? (float*)take(rows * kvd * f) : nullptr;
+  b->v = any_unfused_qkv ? (float*)take(rows * kvd * f) : nullptr;
+  b->attn = (float*)take(rows * qd * f);
+  b->ffn = (float*)take(rows * hid * f);
+  b->gate = any_unfused_glu ? (float*)take(rows * hid * f) : nullptr;
+  b->up = any_unfused_glu ? (float*)take(rows * hid * f) : nullptr;
+  b->apart = (float*)take(attention_workspace_bytes(m->n_heads, m->head_dim, m->max_seq_len,
+                                                    std::min(n, kPrefillAttnRows)));
+  b->lin_bytes = lin;
+  b->lin = take(lin);
   b->total = off;
   return MLQ_OK;
 }
@@ -417,6 +493,134 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
   }
   // computeLogitsDevice (src/forward.cc:736-745)
   return norm_linear(m->lm_head, b.x, m->final_norm, logits, nullptr, MLQ_EPI_NONE);
+}
+
+int mlq_prefill_workspace(const mlq_model* m, int n_tokens, size_t* bytes) {
+  if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
+  PrefillBuffers b;
+  const int rc = plan_prefill(m, n_tokens, nullptr, &b);
+  if (rc != MLQ_OK) return rc;
+  *bytes = b.total;
+  return MLQ_OK;
+}
+
+int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens, int n_tokens,
+                int start_pos, float* logits, void* ws, size_t ws_bytes, mlq_stream_t stream) {
+  PrefillBuffers b;
+  int rc = plan_prefill(m, n_tokens, (char*)ws, &b);
+  if (rc != MLQ_OK) return rc;
+  if ((rc = check_cache(c)) != MLQ_OK) return rc;
+  if (tokens == nullptr || logits == nullptr || ws == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (((uintptr_t)ws & 255u) != 0) return MLQ_ERR_INVALID_ARG;
+  if (ws_bytes < b.total) return MLQ_ERR_BUFFER_TOO_SMALL;
+  if (c->n_layers != m->n_layers || c->n_kv_heads != m->n_kv_heads ||
+      c->head_dim != m->head_dim || c->max_seq_len < m->max_seq_len)
+    return MLQ_ERR_SHAPE;
+  // forwardBatch / validateForwardInputs (src/batch.cc:32-55,
+  // src/forward.cc:27-58) for every token of the batch
+  if (start_pos < 0 || start_pos > m->max_seq_len - n_tokens) return MLQ_ERR_INVALID_ARG;
+  for (int i = 0; i < n_tokens; ++i)
+    if (tokens[i] < 0 || tokens[i] >= m->vocab_size) return MLQ_ERR_INVALID_ARG;
+
+  const hipStream_t s = (hipStream_t)stream;
+  const int n = n_tokens, dim = m->dim, hd = m->head_dim, hid = m->hidden_dim;
+  const int qd = m->n_heads * hd, kvd = m->n_kv_heads * hd;
+  auto hip = [](hipError_t e) { return record_hip(e); };
+  auto linear = [&](const mlq_weight& w, const float* x, float* y, int rows, const float* bias,
+                    int act) {
+    return mlq_linear_epi(&w, x, y, rows, bias, act, b.lin, b.lin_bytes, stream);
+  };
+  if ((rc = hip(hipMemcpyAsync(b.tokens, tokens, (size_t)n * sizeof(int32_t),
+                               hipMemcpyHostToDevice, s))) != MLQ_OK)
+    return rc;
+  if ((rc = hip(launch_embedding_rows(m->token_embedding, dim, b.tokens, n, b.x, s))) != MLQ_OK)
+    return rc;
+  for (int li = 0; li < m->n_layers; ++li) {
+    const mlq_layer& l = m->layers[li];
+    if ((rc = hip(launch_rmsnorm(b.x, l.attn_norm, b.h, n, dim, m->rms_norm_eps, s))) != MLQ_OK)
+      return rc;
+    RopeRows rr;
+    if (qkv_fused(l)) {
+      if ((rc = linear(l.wq, b.h, b.qkv, n, l.bq, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      rr.q = b.qkv;
+      rr.k = b.qkv + qd;
+      rr.v = b.qkv + qd + kvd;
+      rr.q_stride = rr.k_stride = rr.v_stride = qd + 2 * kvd;
+    } else {
+      if ((rc = linear(l.wq, b.h, b.qkv, n, l.bq, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = linear(l.wk, b.h, b.k, n, l.bk, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = linear(l.wv, b.h, b.v, n, l.bv, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      rr.q = b.qkv;
+      rr.k = b.k;
+      rr.v = b.v;
+      rr.q_stride = qd;
+      rr.k_stride = rr.v_stride = kvd;
+    }
+    rr.rows = n;
+    rr.keys = c->keys;
+    rr.values = c->values;
+    rr.n_heads = m->n_heads;
+    rr.n_kv = m->n_kv_heads;
+    rr.hd = hd;
+    rr.neox = m->rope_type == MLQ_ROPE_NEOX;
+    rr.layer = li;
+    rr.max_seq = c->max_seq_len;
+    rr.pos0 = start_pos;
+    rr.theta = m->rope_theta;
+    if ((rc = hip(launch_rope_rows(rr, s))) != MLQ_OK) return rc;
+    // causal attention: query row r sees cache positions 0..start_pos + r
+    for (int r0 = 0; r0 < n; r0 += kPrefillAttnRows) {
+      const int nr = std::min(kPrefillAttnRows, n - r0);
+      AttnLaunch a;
+      a.q = rr.q + (size_t)r0 * rr.q_stride;
+      a.keys = c->keys;
+      a.values = c->values;
+      a.out = b.attn + (size_t)r0 * qd;
+      a.ws = b.apart;
+      a.layer = li;
+      a.max_seq = c->max_seq_len;
+      a.n_heads = m->n_heads;
+      a.n_kv = m->n_kv_heads;
+      a.hd = hd;
+      a.pos = start_pos + r0;
+      a.max_len = start_pos + r0 + nr;
+      a.rows = nr;
+      a.q_stride = rr.q_stride;
+      a.out_stride = qd;
+      if ((rc = hip(launch_attention(a, s))) != MLQ_OK) return rc;
+    }
+    // x2 = x + wo . attn (per-row residual: a separate add)
+    if ((rc = linear(l.wo, b.attn, b.x2, n, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+    if ((rc = hip(launch_eltwise(kEltAdd, b.x, b.x2, b.x2, (int64_t)n * dim, s))) != MLQ_OK)
+      return rc;
+    if ((rc = hip(launch_rmsnorm(b.x2, l.ffn_norm, b.h, n, dim, m->rms_norm_eps, s))) != MLQ_OK)
+      return rc;
+    if (glu_fused(l)) {
+      if ((rc = linear(l.w_gate, b.h, b.ffn, n, nullptr, MLQ_EPI_SWIGLU)) != MLQ_OK) return rc;
+    } else {
+      if ((rc = linear(l.w_gate, b.h, b.gate, n, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = linear(l.w_up, b.h, b.up, n, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = hip(launch_eltwise(kEltSwiGLU, b.gate, b.up, b.ffn, (int64_t)n * hid, s))) !=
+          MLQ_OK)
+        return rc;
+    }
+    // x = x2 + w_down . ffn
+    if ((rc = linear(l.w_down, b.ffn, b.h, n, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+    if ((rc = hip(launch_eltwise(kEltAdd, b.x2, b.h, b.x, (int64_t)n * dim, s))) != MLQ_OK)
+      return rc;
+  }
+  // logits of the last token only (forwardBatch returns those)
+  const float* last = b.x + (size_t)(n - 1) * dim;
+  const mlq_weight& w = m->lm_head;
+  if (w.type != MLQ_F32 && w.k <= gemv_max_k(w.type, 1) && gemv_norm_supported(w)) {
+    Epilogue e;
+    e.norm = m->final_norm;
+    e.norm_eps = m->rms_norm_eps;
+    return hip(launch_gemv(w, last, logits, 1, s, e));
+  }
+  if ((rc = hip(launch_rmsnorm(last, m->final_norm, b.h, 1, dim, m->rms_norm_eps, s))) != MLQ_OK)
+    return rc;
+  return linear(w, b.h, logits, 1, nullptr, MLQ_EPI_NONE);
 }
 
 }  // extern "C"

@@ -237,6 +237,63 @@ __global__ __launch_bounds__(256) void kv_write_kernel(float* __restrict__ keys,
   values[row + i] = v[i];
 }
 
+// Prefill: RoPE of `rows` consecutive positions pos0 + r (row r of q, k and
+// v at their row strides); q rotated in place, rotated k and v written to
+// cache rows (layer, pos0 + r). Same arithmetic as rope_kernel.
+struct RopeRowsArgs {
+  float* q;
+  float* k;
+  const float* v;
+  int q_stride, k_stride, v_stride, rows;
+  float* keys;
+  float* values;
+  int n_heads, n_kv, hd, neox, layer, max_seq, pos0;
+  float theta;
+};
+
+__global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
+  const int half = a.hd >> 1;
+  const int per_row = (a.n_heads + a.n_kv) * half;
+  const int r = blockIdx.y;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= per_row) return;
+  const int pos = a.pos0 + r;
+  const int head = p / half;
+  const int i = p - head * half;
+  const int i0 = a.neox ? i : 2 * i;
+  const int i1 = a.neox ? i + half : 2 * i + 1;
+  const float freq = 1.0f / powf(a.theta, (float)(2 * i) / (float)a.hd);
+  float sn, c;
+  sincosf((float)pos * freq, &sn, &c);
+  const bool is_q = head < a.n_heads;
+  const int kh = head - a.n_heads;
+  float* xr = is_q ? a.q + (size_t)r * a.q_stride + (size_t)head * a.hd
+                   : a.k + (size_t)r * a.k_stride + (size_t)kh * a.hd;
+  const float x0 = xr[i0], x1 = xr[i1];
+  const float y0 = x0 * c - x1 * sn;
+  const float y1 = x0 * sn + x1 * c;
+  if (is_q) {
+    xr[i0] = y0;
+    xr[i1] = y1;
+    return;
+  }
+  const size_t crow = (((size_t)a.layer * a.max_seq + pos) * a.n_kv + kh) * a.hd;
+  a.keys[crow + i0] = y0;
+  a.keys[crow + i1] = y1;
+  const float* vr = a.v + (size_t)r * a.v_stride + (size_t)kh * a.hd;
+  a.values[crow + i0] = vr[i0];
+  a.values[crow + i1] = vr[i1];
+}
+
+// Prefill: embedding rows y[r] = table[tokens[r]] (tokens checked by the host).
+__global__ __launch_bounds__(256) void embed_rows_kernel(const float* __restrict__ table,
+                                                         int dim, const int32_t* tokens,
+                                                         float* __restrict__ y) {
+  const int r = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < dim) y[(size_t)r * dim + i] = table[(size_t)tokens[r] * dim + i];
+}
+
 // ---- decode attention ----------------------------------------------------------------
 // softmax(q . K^T / sqrt(hd)) . V for one query position against cache
 // positions 0..pos of one layer, query head h reading kv head h / group
@@ -278,6 +335,10 @@ struct AttnArgs {
   float* part;          // workspace: m, l [n_heads][chunks]; acc [n_heads][chunks][hd]
   int layer, max_seq, n_kv, hd, group, chunks, chunk_len;
   int vec;              // K/V rows are float4-aligned (hd % 4 == 0, aligned cache)
+  // Query rows (grid z): row r sits at position pos + r and reads q at
+  // q + r * q_stride, writes out + r * out_stride; partials are [rows] x
+  // [n_heads] x [chunks]. One row for a decode step.
+  int rows, q_stride, out_stride;
   const int32_t* pos_dev;
   int pos;
   float scale;
@@ -294,6 +355,22 @@ struct AttnArgs {
   int neox;
 };
 
+// Partial arrays of query row r: m and l [n_heads][chunks], acc
+// [n_heads][chunks][hd], each array holding every row.
+struct Partials {
+  float* m;
+  float* l;
+  float* acc;
+};
+__device__ __forceinline__ Partials partials_of(const AttnArgs& a, int r) {
+  const size_t per = (size_t)a.group * a.n_kv * a.chunks;  // n_heads * chunks
+  Partials p;
+  p.m = a.part + (size_t)r * per;
+  p.l = a.part + (size_t)a.rows * per + (size_t)r * per;
+  p.acc = a.part + 2 * (size_t)a.rows * per + (size_t)r * per * a.hd;
+  return p;
+}
+
 template <int HD, int GMAX>
 __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
   constexpr int CH = kAttnLdsChunk;
@@ -305,7 +382,8 @@ __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
   float* qs = lds + CH * stride;       // [GMAX][hdp]
   float* ps = qs + GMAX * hdp;         // [GMAX][CH]
 
-  const int pos = read_scalar(a.pos_dev, a.pos);
+  const int qrow = blockIdx.z;
+  const int pos = read_scalar(a.pos_dev, a.pos) + qrow;
   const int len = pos + 1;
   const int t0 = blockIdx.x * CH;
   if (pos < 0 || pos >= a.max_seq || t0 >= len) return;
@@ -313,6 +391,7 @@ __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
   const int kvh = blockIdx.y;
   const int lane = threadIdx.x;
   const int G = a.group;
+  const float* qrow_ptr = a.q + (size_t)qrow * a.q_stride;
   const size_t row_stride = (size_t)a.n_kv * hd;
   const size_t base = ((size_t)a.layer * a.max_seq + t0) * row_stride + (size_t)kvh * hd;
 
@@ -336,7 +415,7 @@ __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
   for (int i = lane; i < G * hdp; i += 64) {
     const int g = i / hdp;
     const int c = i - g * hdp;
-    qs[i] = c < hd ? a.q[(size_t)(kvh * G + g) * hd + c] : 0.0f;
+    qs[i] = c < hd ? qrow_ptr[(size_t)(kvh * G + g) * hd + c] : 0.0f;
   }
   stage(a.keys);
   __syncthreads();
@@ -399,9 +478,10 @@ __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
     }
   }
   const int chunk = blockIdx.x;
-  float* pm = a.part;
-  float* pl = a.part + (size_t)a.group * a.n_kv * a.chunks;
-  float* pa = pl + (size_t)a.group * a.n_kv * a.chunks;
+  const Partials pp = partials_of(a, qrow);
+  float* pm = pp.m;
+  float* pl = pp.l;
+  float* pa = pp.acc;
 #pragma unroll
   for (int g = 0; g < GMAX; ++g) {
     if (g < G) {
@@ -445,7 +525,8 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
   __shared__ float wm[W][GMAX], wl[W][GMAX];
   __shared__ float wacc[W][GMAX][HD];
 
-  const int pos = read_scalar(a.pos_dev, a.pos);
+  const int qrow = blockIdx.z;
+  const int pos = read_scalar(a.pos_dev, a.pos) + qrow;
   const int len = pos + 1;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -482,7 +563,7 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
   // below runs a fixed GMAX times with no per-head branches (their results
   // are never stored), which lets the heads' reductions interleave
   if constexpr (FUSED) {
-    const float* qraw = a.q + (size_t)kvh * G * HD;
+    const float* qraw = a.q + (size_t)qrow * a.q_stride + (size_t)kvh * G * HD;
     float* qf = (float*)qs;
     for (int i = threadIdx.x; i < GMAX * HD; i += W * 64) {
       const int g = i / HD;
@@ -508,7 +589,7 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
       }
     }
   } else {
-    const f4_t* q4 = (const f4_t*)(a.q + (size_t)kvh * G * HD);
+    const f4_t* q4 = (const f4_t*)(a.q + (size_t)qrow * a.q_stride + (size_t)kvh * G * HD);
     for (int i = threadIdx.x; i < GMAX * HD / 4; i += W * 64)
       qs[i] = i < G * HD / 4 ? q4[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
@@ -583,10 +664,10 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
   }
   __syncthreads();
   const int chunk = blockIdx.x;
-  const int n_heads = G * a.n_kv;
-  float* pm = a.part;
-  float* pl = a.part + (size_t)n_heads * a.chunks;
-  float* pa = pl + (size_t)n_heads * a.chunks;
+  const Partials pp = partials_of(a, qrow);
+  float* pm = pp.m;
+  float* pl = pp.l;
+  float* pa = pp.acc;
   for (int g = wave; g < G; g += W) {
     float mx = -INFINITY;
 #pragma unroll
@@ -621,19 +702,20 @@ constexpr int kCombineBatch = 32;
 
 __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   __shared__ float wsh[kCombineBatch];
-  const int pos = read_scalar(a.pos_dev, a.pos);
+  const int qrow = blockIdx.y;
+  const int pos = read_scalar(a.pos_dev, a.pos) + qrow;
   const int head = blockIdx.x;
   const int lane = threadIdx.x;
-  const int n_heads = a.group * a.n_kv;
-  float* out = a.out + (size_t)head * a.hd;
+  float* out = a.out + (size_t)qrow * a.out_stride + (size_t)head * a.hd;
   if (pos < 0 || pos >= a.max_seq) {  // only reachable through a device position
     for (int d = lane; d < a.hd; d += 64) out[d] = __builtin_nanf("");
     return;
   }
   const int chunks = (pos + a.chunk_len) / a.chunk_len;
-  const float* pm = a.part + (size_t)head * a.chunks;
-  const float* pl = a.part + (size_t)n_heads * a.chunks + (size_t)head * a.chunks;
-  const float* pa = a.part + 2 * (size_t)n_heads * a.chunks + (size_t)head * a.chunks * a.hd;
+  const Partials pp = partials_of(a, qrow);
+  const float* pm = pp.m + (size_t)head * a.chunks;
+  const float* pl = pp.l + (size_t)head * a.chunks;
+  const float* pa = pp.acc + (size_t)head * a.chunks * a.hd;
   float mx = -INFINITY;
   for (int c = lane; c < chunks; c += 64) mx = fmaxf(mx, pm[c]);
   mx = wave_max(mx);
@@ -864,6 +946,38 @@ hipError_t launch_rope(const RopeLaunch& r, hipStream_t stream) {
   return hipGetLastError();
 }
 
+hipError_t launch_rope_rows(const RopeRows& rr, hipStream_t stream) {
+  RopeRowsArgs a;
+  a.q = rr.q;
+  a.k = rr.k;
+  a.v = rr.v;
+  a.q_stride = rr.q_stride;
+  a.k_stride = rr.k_stride;
+  a.v_stride = rr.v_stride;
+  a.rows = rr.rows;
+  a.keys = rr.keys;
+  a.values = rr.values;
+  a.n_heads = rr.n_heads;
+  a.n_kv = rr.n_kv;
+  a.hd = rr.hd;
+  a.neox = rr.neox;
+  a.layer = rr.layer;
+  a.max_seq = rr.max_seq;
+  a.pos0 = rr.pos0;
+  a.theta = rr.theta;
+  const int per_row = (rr.n_heads + rr.n_kv) * (rr.hd / 2);
+  hipLaunchKernelGGL(rope_rows_kernel, dim3((per_row + 255) / 256, rr.rows), dim3(256), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_embedding_rows(const float* table, int dim, const int32_t* tokens, int rows,
+                                 float* y, hipStream_t stream) {
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((dim + 255) / 256, rows), dim3(256), 0, stream,
+                     table, dim, tokens, y);
+  return hipGetLastError();
+}
+
 hipError_t launch_kv_write(float* keys, float* values, const float* k, const float* v,
                            size_t row, int n, hipStream_t stream) {
   hipLaunchKernelGGL(kv_write_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, keys,
@@ -878,9 +992,9 @@ int attention_chunks(int hd, int max_len) {
   return (max_len + ch - 1) / ch;
 }
 
-size_t attention_workspace_bytes(int n_heads, int hd, int max_len) {
+size_t attention_workspace_bytes(int n_heads, int hd, int max_len, int rows) {
   const size_t c = (size_t)attention_chunks(hd, max_len);
-  return ((size_t)n_heads * c * (2 + (size_t)hd)) * sizeof(float);
+  return (size_t)rows * ((size_t)n_heads * c * (2 + (size_t)hd)) * sizeof(float);
 }
 
 // The register kernel (and so the fused RoPE + cache write) covers head
@@ -899,16 +1013,16 @@ template <int HD, int GMAX>
 static void attn_launch(const AttnArgs& a, hipStream_t stream) {
   if constexpr (HD != 0) {
     if (a.rope_cs != nullptr)
-      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, true>), dim3(a.chunks, a.n_kv),
+      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, true>), dim3(a.chunks, a.n_kv, a.rows),
                          dim3(kAttnRegWaves * 64), 0, stream, a);
     else
-      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, false>), dim3(a.chunks, a.n_kv),
+      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, false>), dim3(a.chunks, a.n_kv, a.rows),
                          dim3(kAttnRegWaves * 64), 0, stream, a);
   } else {
     constexpr int CH = kAttnLdsChunk;
     const int hdp = (a.hd + 3) & ~3;
     const size_t lds = (size_t)(CH * (hdp + 4) + GMAX * hdp + GMAX * CH) * sizeof(float);
-    hipLaunchKernelGGL((attn_chunk_kernel<0, GMAX>), dim3(a.chunks, a.n_kv), dim3(64), lds,
+    hipLaunchKernelGGL((attn_chunk_kernel<0, GMAX>), dim3(a.chunks, a.n_kv, a.rows), dim3(64), lds,
                        stream, a);
   }
 }
@@ -929,6 +1043,9 @@ hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   a.values = r.values;
   a.out = r.out;
   a.part = r.ws;
+  a.rows = r.rows;
+  a.q_stride = r.q_stride;
+  a.out_stride = r.out_stride;
   a.layer = r.layer;
   a.max_seq = r.max_seq;
   a.n_kv = r.n_kv;
@@ -958,7 +1075,7 @@ hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(r.n_heads), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(r.n_heads, a.rows), dim3(64), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -144,11 +144,31 @@ struct AttnLaunch {
   const float* v_new = nullptr;
   const float* rope_cs = nullptr;
   int neox = 0;
+  // Several query rows (prefill, rope_cs == nullptr): row r at position
+  // pos + r, q row r at q + r * q_stride, output row at out + r * out_stride;
+  // ws holds attention_workspace_bytes(n_heads, hd, max_len, rows).
+  int rows = 1, q_stride = 0, out_stride = 0;
 };
 bool attention_supported(int n_heads, int n_kv, int hd);
 bool attention_fusable(int hd, int group);
 int attention_chunks(int hd, int max_len);
-size_t attention_workspace_bytes(int n_heads, int hd, int max_len);
+size_t attention_workspace_bytes(int n_heads, int hd, int max_len, int rows = 1);
+// Prefill helpers: RoPE + cache write of `rows` consecutive positions pos0
+// + r (q rotated in place; rotated k and v to the cache), and embedding rows
+// for device tokens.
+struct RopeRows {
+  float* q = nullptr;
+  float* k = nullptr;
+  const float* v = nullptr;
+  int q_stride = 0, k_stride = 0, v_stride = 0, rows = 0;
+  float* keys = nullptr;
+  float* values = nullptr;
+  int n_heads = 0, n_kv = 0, hd = 0, neox = 0, layer = 0, max_seq = 0, pos0 = 0;
+  float theta = 10000.0f;
+};
+hipError_t launch_rope_rows(const RopeRows& rr, hipStream_t stream);
+hipError_t launch_embedding_rows(const float* table, int dim, const int32_t* tokens, int rows,
+                                 float* y, hipStream_t stream);
 hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream);
 // out = argmax(x) (first maximum, NaN never wins); pos_dev += 1 when non-null.
 // One workgroup, no workspace:

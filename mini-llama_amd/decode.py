@@ -182,6 +182,7 @@ class DecodeModel:
         _check(lib().mlq_argmax_workspace(c["vocab_size"], ctypes.byref(nbytes)),
                "mlq_argmax_workspace")
         self.argmax_ws = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        self._prefill_ws = None
 
     @property
     def weight_bytes(self) -> int:
@@ -203,6 +204,25 @@ class DecodeModel:
                                       self.logits.data_ptr(), ws.data_ptr(), ws.numel(),
                                       _stream(stream)),
                "mlq_decode_token")
+        return self.logits
+
+    def prefill(self, tokens, start_pos: int = 0, stream=None):
+        """logits [vocab] of the last of `tokens` after running all of them
+        at positions start_pos.. at once (forwardBatch with [n, K] Linears);
+        their K/V rows land in the cache. Overwritten by the next step."""
+        import torch
+        toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+        nbytes = ctypes.c_size_t()
+        _check(lib().mlq_prefill_workspace(ctypes.byref(self._model), toks.size,
+                                           ctypes.byref(nbytes)), "mlq_prefill_workspace")
+        if self._prefill_ws is None or self._prefill_ws.numel() < nbytes.value:
+            self._prefill_ws = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        ws = self._prefill_ws
+        _check(lib().mlq_prefill(ctypes.byref(self._model), ctypes.byref(self._cache),
+                                 toks.ctypes.data, toks.size, int(start_pos),
+                                 self.logits.data_ptr(), ws.data_ptr(), ws.numel(),
+                                 _stream(stream)),
+               "mlq_prefill")
         return self.logits
 
     def step_device(self, stream=None) -> None:
@@ -241,16 +261,21 @@ class DecodeModel:
                                 _stream(stream)), "mlq_argmax")
         return int(out.item())
 
-    def generate_greedy(self, prompt, n_new: int, graph: bool = True) -> list:
+    def generate_greedy(self, prompt, n_new: int, graph: bool = True,
+                        prefill: bool = False) -> list:
         """The reference's greedy loop (tests/test_forward.cc:53-84): each
-        prompt token at its position, then n_new sampled tokens, each fed
-        back at the next position. Returns the n_new new tokens."""
+        prompt token at its position (or all of them at once with
+        prefill=True), then n_new sampled tokens, each fed back at the next
+        position. Returns the n_new new tokens."""
         import torch
         prompt = [int(t) for t in prompt]
         if not prompt or len(prompt) + n_new > self.config["max_seq_len"]:
             raise ValueError("prompt empty or longer than the cache")
-        for i, t in enumerate(prompt):
-            self.forward_token(t, i)
+        if prefill:
+            self.prefill(prompt, 0)
+        else:
+            for i, t in enumerate(prompt):
+                self.forward_token(t, i)
         self.pos_dev.fill_(len(prompt) - 1)
         self._greedy(_stream(None))
         history = torch.empty(n_new, dtype=torch.int32, device=self.device)

@@ -543,3 +543,99 @@ def test_decode_host_validation(pkg, cuda):
     assert call(1, 128) == -1       # :125-141
     assert call(1, 0, ws_bytes=64) == -4
     assert call(1, 0) == 0
+
+
+# ---- batched prefill ------------------------------------------------------------------------
+PREFILL_CASES = [
+    # (qtype, model kwargs, fuse, start, n)
+    ("q4_0", {"cfg": {"dim": 512, "n_heads": 4, "n_kv_heads": 2, "rope_type": 1}}, True, 0, 130),
+    ("q8_0", {"cfg": {"dim": 512, "n_heads": 8, "n_kv_heads": 2}, "bias": True}, True, 7, 64),
+    ("q4_1", {"cfg": {"dim": 256, "n_heads": 4, "n_kv_heads": 4}}, False, 3, 65),
+    ("f32", {"cfg": {"dim": 128, "n_heads": 4, "n_kv_heads": 2}, "bias": True}, True, 0, 5),
+    ("q4_0", {"cfg": {"dim": 128, "n_heads": 4, "n_kv_heads": 1, "hidden_dim": 100}}, True, 2, 1),
+    ("q4_0", {"cfg": {"dim": 512, "n_heads": 2, "n_kv_heads": 1, "rope_type": 1}}, True, 0, 9),
+]
+
+
+@pytest.mark.parametrize("qtype,kw,fuse,start,n", PREFILL_CASES)
+def test_prefill_matches_sequential_oracle(pkg, oracle, cuda, qtype, kw, fuse, start, n):
+    """mlq_prefill of n tokens after `start` decode steps against the
+    oracle's forwardBatch (one forward_token per token): the last logits,
+    every K/V row, and decode steps after it. Tolerance: n > 8 runs the
+    skinny / prefill GEMMs on fp16-rounded activations (about 1e-4 of the
+    scale per Linear, here through two layers and the residuals): 2e-3 of
+    max|logit|; n <= 8 keeps the decode GEMV's fp32-class 1e-4."""
+    import mini_llama_amd.decode as dec
+    import mini_llama_amd.synth as synth
+    kw = dict(kw)
+    cfg = dict(vocab_size=160, dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=2,
+               max_seq_len=160)
+    cfg.update(kw.pop("cfg", {}))
+    model = synth.synthetic_model(cfg, qtype, seed=21, **kw)
+    rng = np.random.default_rng(n + start)
+    tokens = rng.integers(0, cfg["vocab_size"], start + n + 3).tolist()
+    dm = dec.DecodeModel(model, fuse=fuse)
+    cache = oracle.new_cache(model)
+    for p in range(start):
+        oracle.forward_token(model, cache, tokens[p], p)
+        dm.forward_token(tokens[p], p)
+    for p in range(start, start + n):
+        ref = oracle.forward_token(model, cache, tokens[p], p)
+    got = dm.prefill(tokens[start:start + n], start).cpu().numpy()
+    rel = 2e-3 if n > 8 and qtype != "f32" else 1e-4
+    scale = np.abs(ref).max()
+    err = np.abs(got - ref).max()
+    print(f"prefill {qtype} n={n} start={start}: logits error / max = {err / scale:.2e}")
+    assert err <= rel * scale + 1e-6
+    keys, values = dm.keys.cpu().numpy(), dm.values.cpu().numpy()
+    end = start + n
+    for arr, want in ((keys, cache[0]), (values, cache[1])):
+        amax = np.abs(want[:, :end]).max()
+        assert np.abs(arr[:, :end] - want[:, :end]).max() <= rel * 10 * amax + 2.4e-7 * end * amax
+        assert not arr[:, end:].any()
+    # decode continues from the prefilled cache
+    for p in range(end, end + 3):
+        ref = oracle.forward_token(model, cache, tokens[p], p)
+        got = dm.forward_token(tokens[p], p).cpu().numpy()
+        assert np.abs(got - ref).max() <= rel * np.abs(ref).max() + 1e-6, p
+
+
+def test_prefill_tiny_model_greedy(pkg, oracle, cuda):
+    """The reference's tiny model (F32 weights): greedy generation with the
+    prompt prefilled in one batch picks the oracle's tokens."""
+    import mini_llama_amd.decode as dec
+    model = _tiny(pkg)
+    prompt = [1] + list(b"hello world")
+    cache = oracle.new_cache(model)
+    for p, t in enumerate(prompt):
+        logits = oracle.forward_token(model, cache, t, p)
+    want, nxt = [], oracle.argmax(logits)
+    for step in range(4):
+        want.append(nxt)
+        logits = oracle.forward_token(model, cache, nxt, len(prompt) + step)
+        nxt = oracle.argmax(logits)
+    dm = dec.DecodeModel(model)
+    assert dm.generate_greedy(prompt, 4, prefill=True) == want
+
+
+def test_prefill_host_validation(pkg, cuda):
+    import mini_llama_amd.decode as dec
+    dm = dec.DecodeModel(_tiny(pkg))
+    lib = pkg.lib()
+    nbytes = ctypes.c_size_t()
+    assert lib.mlq_prefill_workspace(ctypes.byref(dm._model), 0, ctypes.byref(nbytes)) == -2
+    _ok(pkg, lib.mlq_prefill_workspace(ctypes.byref(dm._model), 4, ctypes.byref(nbytes)), "ws")
+    import torch
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=cuda)
+
+    def call(toks, start, ws_bytes=None):
+        t = np.asarray(toks, np.int32)
+        return lib.mlq_prefill(ctypes.byref(dm._model), ctypes.byref(dm._cache), t.ctypes.data,
+                               t.size, start, dm.logits.data_ptr(), ws.data_ptr(),
+                               ws.numel() if ws_bytes is None else ws_bytes, _s(pkg))
+    assert call([1, 2, 128, 3], 0) == -1
+    assert call([1, 2, 3, -1], 0) == -1
+    assert call([1, 2, 3, 4], 125) == -1      # 125 + 4 > max_seq_len 128
+    assert call([1, 2, 3, 4], -1) == -1
+    assert call([1, 2, 3, 4], 0, ws_bytes=100) == -4
+    assert call([1, 2, 3, 4], 124) == 0
