@@ -568,8 +568,29 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
     rr.pos0 = start_pos;
     rr.theta = m->rope_theta;
     if ((rc = hip(launch_rope_rows(rr, s))) != MLQ_OK) return rc;
-    // causal attention: query row r sees cache positions 0..start_pos + r
-    for (int r0 = 0; r0 < n; r0 += kPrefillAttnRows) {
+    // causal attention: query row r sees cache positions 0..start_pos + r;
+    // MFMA tiles of query rows where the head dims allow, else the decode
+    // kernel over blocks of query rows
+    const bool mfma_attn = prefill_attention_supported(hd, m->n_heads / m->n_kv_heads) &&
+                           ((uintptr_t)c->keys & 15) == 0 && ((uintptr_t)c->values & 15) == 0;
+    if (mfma_attn) {
+      AttnLaunch a;
+      a.q = rr.q;
+      a.keys = c->keys;
+      a.values = c->values;
+      a.out = b.attn;
+      a.layer = li;
+      a.max_seq = c->max_seq_len;
+      a.n_heads = m->n_heads;
+      a.n_kv = m->n_kv_heads;
+      a.hd = hd;
+      a.pos = start_pos;
+      a.rows = n;
+      a.q_stride = rr.q_stride;
+      a.out_stride = qd;
+      if ((rc = hip(launch_attention_prefill(a, s))) != MLQ_OK) return rc;
+    }
+    for (int r0 = 0; !mfma_attn && r0 < n; r0 += kPrefillAttnRows) {
       const int nr = std::min(kPrefillAttnRows, n - r0);
       AttnLaunch a;
       a.q = rr.q + (size_t)r0 * rr.q_stride;

@@ -694,6 +694,160 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
   }
 }
 
+// ---- prefill attention (many query rows) -----------------------------------------------
+// Causal attention of query rows pos0 + r (r < rows) on fp32 MFMA
+// (v_mfma_f32_16x16x4f32: exact fp32 products). A wave owns one tile of 16
+// (query row, head) pairs that read the same kv head: QT = 16 / GP rows
+// times GP heads (the group padded to a power of two; padding heads are
+// zero and never stored). It walks the keys in chunks of 16 up to the
+// tile's last position, with the next chunk's K / V rows loaded while the
+// current one is used:
+//   S = Q K^T: HD/4 MFMA steps, A = q (registers), B = K chunk (LDS);
+//   scale, causal mask, online softmax per row (D-layout rows live in one
+//   16-lane DPP row: row max / sum without LDS);
+//   O += P V: P goes through LDS into the A layout, B = V chunk (LDS),
+//   HD/16 output tiles x 4 steps.
+// MFMA layouts (16x16x4 f32): A[i][k] from lane i + 16k, B[k][j] from lane
+// j + 16k, D[4*(l/16) + r][l % 16] in register r of lane l.
+// Waves (tiles) per workgroup: two, one at head_dim 256 (LDS per wave).
+__host__ __device__ constexpr int prefill_waves(int hd) { return hd == 256 ? 1 : 2; }
+
+template <int HD, int GP>
+__global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(AttnArgs a) {
+  constexpr int kPrefillWaves = prefill_waves(HD);
+  constexpr int QT = 16 / GP;   // query rows per tile
+  constexpr int KC = 16;        // keys per chunk
+  constexpr int NT = HD / 16;   // output tiles
+  constexpr int KS = HD + 1;    // padded LDS row of K (conflict-free B reads)
+  constexpr int KF4 = KC * HD / 4 / 64;  // float4 of a chunk per lane
+  __shared__ float ksh[kPrefillWaves][KC * KS];
+  __shared__ float vsh[kPrefillWaves][KC * HD];
+  __shared__ float psh[kPrefillWaves][16 * 17];
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int kvh = blockIdx.y;
+  const int G = a.group;
+  const int r0 = (blockIdx.x * kPrefillWaves + wave) * QT;  // first query row of the tile
+  if (r0 >= a.rows) return;  // (waves share no barrier)
+  const int pos0 = a.pos;
+  const int last_row = min(r0 + QT, a.rows) - 1;
+  const int kmax = pos0 + last_row;  // last key any row of the tile sees
+  const size_t row_stride = (size_t)a.n_kv * HD;
+  const size_t cbase = (size_t)a.layer * a.max_seq * row_stride + (size_t)kvh * HD;
+  float* kw = ksh[wave];
+  float* vw = vsh[wave];
+  float* pw = psh[wave];
+
+  // A operand: row i = lane % 16 of the tile, dims 4s + lane / 16
+  const int ai = lane & 15, ak = lane >> 4;
+  const int aq = r0 + ai / GP, ag = ai % GP;
+  const bool arow = aq < a.rows && ag < G;
+  const float* qp = a.q + (size_t)(arow ? aq : 0) * a.q_stride + (size_t)(kvh * G + (arow ? ag : 0)) * HD;
+  float qa[HD / 4];
+#pragma unroll
+  for (int st = 0; st < HD / 4; ++st) qa[st] = arow ? qp[4 * st + ak] : 0.0f;
+
+  // D-layout rows of this lane: 4 * (lane / 16) + i
+  int dq[4], dpos[4];
+  bool dvalid[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 4 * (lane >> 4) + i;
+    dq[i] = r0 + m / GP;
+    dvalid[i] = dq[i] < a.rows && (m % GP) < G;
+    dpos[i] = pos0 + dq[i];
+  }
+  float mrow[4], lrow[4];
+  f4_t acc[NT];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    mrow[i] = -INFINITY;
+    lrow[i] = 0.0f;
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto load_chunk = [&](int k0, f4_t* kr, f4_t* vr) {
+#pragma unroll
+    for (int u = 0; u < KF4; ++u) {
+      const int f = lane + 64 * u;       // float4 index in the chunk
+      const int key = f / (HD / 4);
+      const int c4 = f - key * (HD / 4);
+      const size_t off = cbase + (size_t)min(k0 + key, kmax) * row_stride + 4 * c4;
+      kr[u] = *(const f4_t*)(a.keys + off);
+      vr[u] = *(const f4_t*)(a.values + off);
+    }
+  };
+  f4_t kn[KF4], vn[KF4];
+  load_chunk(0, kn, vn);
+  for (int k0 = 0; k0 <= kmax; k0 += KC) {
+    // this chunk's rows to LDS, the next chunk's loads in flight
+#pragma unroll
+    for (int u = 0; u < KF4; ++u) {
+      const int f = lane + 64 * u;
+      const int key = f / (HD / 4);
+      const int c4 = f - key * (HD / 4);
+      float* kd = kw + key * KS + 4 * c4;
+      kd[0] = kn[u].x;
+      kd[1] = kn[u].y;
+      kd[2] = kn[u].z;
+      kd[3] = kn[u].w;
+      *(f4_t*)(vw + key * HD + 4 * c4) = vn[u];
+    }
+    if (k0 + KC <= kmax) load_chunk(k0 + KC, kn, vn);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes landed
+    __builtin_amdgcn_wave_barrier();
+
+    // S = Q K^T for keys k0 .. k0 + 15
+    f4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < HD / 4; ++st)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], kw[(lane & 15) * KS + 4 * st + ak],
+                                                  sacc, 0, 0, 0);
+    const int key = k0 + (lane & 15);
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = dvalid[i] && key <= dpos[i];
+      const float sc = ok ? sacc[i] * a.scale : -INFINITY;
+      const float mx = fmaxf(mrow[i], row_max<16>(sc));
+      // rows with nothing visible yet keep m = -inf and weight 0
+      const float alpha = mx == -INFINITY ? 1.0f : expf(mrow[i] - mx);
+      const float p = ok ? expf(sc - mx) : 0.0f;
+      lrow[i] = lrow[i] * alpha + row_sum<16>(p);
+      mrow[i] = mx;
+      pr[i] = p;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t][i] *= alpha;
+    }
+    // P (D layout) -> LDS -> A layout
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pw[(4 * (lane >> 4) + i) * 17 + (lane & 15)] = pr[i];
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    float pa[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) pa[st] = pw[(lane & 15) * 17 + 4 * st + ak];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+            pa[st], vw[(4 * st + ak) * HD + 16 * t + (lane & 15)], acc[t], 0, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // reads of this chunk done before the next writes
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (!dvalid[i]) continue;
+    const int m = 4 * (lane >> 4) + i;
+    float* o = a.out + (size_t)dq[i] * a.out_stride + (size_t)(kvh * G + m % GP) * HD;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) o[16 * t + (lane & 15)] = acc[t][i] / lrow[i];
+  }
+}
+
 // Pass 2: one wave per query head. Lanes take chunks for the global max and
 // the rescaled sum; the weights exp(m_c - M) go through LDS 32 chunks at a
 // time, and lanes over head dims load those 32 partials at once (predicated,
@@ -1076,6 +1230,55 @@ hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(r.n_heads, a.rows), dim3(64), 0, stream, a);
+  return hipGetLastError();
+}
+
+bool prefill_attention_supported(int hd, int group) {
+  return (hd == 64 || hd == 128 || hd == 256) && group >= 1 && group <= 16;
+}
+
+template <int HD, int GP>
+static void prefill_launch(const AttnArgs& a, hipStream_t stream) {
+  constexpr int QT = 16 / GP;
+  constexpr int W = prefill_waves(HD);
+  const int tiles = (a.rows + QT - 1) / QT;
+  hipLaunchKernelGGL((attn_prefill_kernel<HD, GP>), dim3((tiles + W - 1) / W, a.n_kv),
+                     dim3(W * 64), 0, stream, a);
+}
+
+template <int HD>
+static void prefill_launch_g(const AttnArgs& a, hipStream_t stream) {
+  if (a.group <= 1) prefill_launch<HD, 1>(a, stream);
+  else if (a.group <= 2) prefill_launch<HD, 2>(a, stream);
+  else if (a.group <= 4) prefill_launch<HD, 4>(a, stream);
+  else if (a.group <= 8) prefill_launch<HD, 8>(a, stream);
+  else prefill_launch<HD, 16>(a, stream);
+}
+
+hipError_t launch_attention_prefill(const AttnLaunch& r, hipStream_t stream) {
+  AttnArgs a = {};
+  a.q = r.q;
+  a.keys = r.keys;
+  a.values = r.values;
+  a.out = r.out;
+  a.layer = r.layer;
+  a.max_seq = r.max_seq;
+  a.n_kv = r.n_kv;
+  a.hd = r.hd;
+  a.group = r.n_heads / r.n_kv;
+  a.pos = r.pos;
+  a.rows = r.rows;
+  a.q_stride = r.q_stride;
+  a.out_stride = r.out_stride;
+  a.scale = sqrtf(1.0f / (float)r.hd);
+  if (!prefill_attention_supported(r.hd, a.group) || ((uintptr_t)r.keys & 15) != 0 ||
+      ((uintptr_t)r.values & 15) != 0)
+    return hipErrorInvalidValue;
+  switch (r.hd) {
+    case 64: prefill_launch_g<64>(a, stream); break;
+    case 128: prefill_launch_g<128>(a, stream); break;
+    default: prefill_launch_g<256>(a, stream); break;
+  }
   return hipGetLastError();
 }
 

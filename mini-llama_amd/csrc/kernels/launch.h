@@ -153,6 +153,11 @@ bool attention_supported(int n_heads, int n_kv, int hd);
 bool attention_fusable(int hd, int group);
 int attention_chunks(int hd, int max_len);
 size_t attention_workspace_bytes(int n_heads, int hd, int max_len, int rows = 1);
+// Prefill attention on fp32 MFMA: rows query rows at positions pos + r,
+// causal, for head_dim 64 / 128 / 256 and 16-byte aligned caches (else
+// hipErrorInvalidValue); no workspace.
+bool prefill_attention_supported(int hd, int group);
+hipError_t launch_attention_prefill(const AttnLaunch& r, hipStream_t stream);
 // Prefill helpers: RoPE + cache write of `rows` consecutive positions pos0
 // + r (q rotated in place; rotated k and v to the cache), and embedding rows
 // for device tokens.
