@@ -696,57 +696,62 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
 
 // ---- prefill attention (many query rows) -----------------------------------------------
 // Causal attention of query rows pos0 + r (r < rows) on fp32 MFMA
-// (v_mfma_f32_16x16x4f32: exact fp32 products). A wave owns one tile of 16
-// (query row, head) pairs that read the same kv head: QT = 16 / GP rows
-// times GP heads (the group padded to a power of two; padding heads are
-// zero and never stored). It walks the keys in chunks of 16 up to the
-// tile's last position, with the next chunk's K / V rows loaded while the
-// current one is used:
-//   S = Q K^T: HD/4 MFMA steps, A = q (registers), B = K chunk (LDS);
-//   scale, causal mask, online softmax per row (D-layout rows live in one
-//   16-lane DPP row: row max / sum without LDS);
-//   O += P V: P goes through LDS into the A layout, B = V chunk (LDS),
-//   HD/16 output tiles x 4 steps.
+// (v_mfma_f32_16x16x4f32: exact fp32 products). A workgroup owns one tile of
+// 16 (query row, head) pairs that read the same kv head: QT = 16 / GP rows
+// times GP heads (the group padded to a power of two; padding heads are zero
+// and never stored). Its W waves split the tile's key chunks (16 keys;
+// wave w takes chunks w, w + W, ...) so the causal triangle's long rows do
+// not serialise on one wave, and merge their (max, sum, acc) in LDS at the
+// end. Per chunk a wave:
+//   stages K (float4 loads, next chunk loaded ahead) into its LDS slab;
+//   S = Q K^T: HD/4 MFMA steps in four independent chains, A = q
+//   (registers), B = K (LDS float4 reads: the k index of step st is head dim
+//   (lane / 16) * HD/4 + st, contiguous per lane);
+//   scales, masks (key <= row position), online softmax per row (a D-layout
+//   row lives in one 16-lane DPP row);
+//   O += P V: P through LDS into the A layout, B = V straight from the
+//   cache (L2-hot; loaded ahead with K at head_dim <= 128), HD/16 tiles x 4.
 // MFMA layouts (16x16x4 f32): A[i][k] from lane i + 16k, B[k][j] from lane
 // j + 16k, D[4*(l/16) + r][l % 16] in register r of lane l.
-// Waves (tiles) per workgroup: two, one at head_dim 256 (LDS per wave).
-__host__ __device__ constexpr int prefill_waves(int hd) { return hd == 256 ? 1 : 2; }
+__host__ __device__ constexpr int prefill_waves(int hd) { return hd == 256 ? 2 : 4; }
 
 template <int HD, int GP>
 __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(AttnArgs a) {
-  constexpr int kPrefillWaves = prefill_waves(HD);
+  constexpr int W = prefill_waves(HD);
   constexpr int QT = 16 / GP;   // query rows per tile
   constexpr int KC = 16;        // keys per chunk
   constexpr int NT = HD / 16;   // output tiles
-  constexpr int KS = HD + 1;    // padded LDS row of K (conflict-free B reads)
-  constexpr int KF4 = KC * HD / 4 / 64;  // float4 of a chunk per lane
-  __shared__ float ksh[kPrefillWaves][KC * KS];
-  __shared__ float vsh[kPrefillWaves][KC * HD];
-  __shared__ float psh[kPrefillWaves][16 * 17];
+  constexpr int KS = HD + 4;    // padded LDS row of K (16-byte aligned)
+  constexpr int KF4 = KC * HD / 4 / 64;  // float4 of a K chunk per lane
+  constexpr bool VPRE = HD <= 128;       // V of the next chunk loaded ahead
+  constexpr int SLAB = KC * KS + 16 * 17;          // per wave: K chunk + P
+  constexpr int MERGE = W * (16 * HD + 32);        // partial acc + max / sum
+  constexpr int LDSF = W * SLAB > MERGE ? W * SLAB : MERGE;
+  __shared__ __align__(16) float lds[LDSF];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int kvh = blockIdx.y;
   const int G = a.group;
-  const int r0 = (blockIdx.x * kPrefillWaves + wave) * QT;  // first query row of the tile
-  if (r0 >= a.rows) return;  // (waves share no barrier)
+  const int r0 = blockIdx.x * QT;  // first query row of the tile
   const int pos0 = a.pos;
   const int last_row = min(r0 + QT, a.rows) - 1;
   const int kmax = pos0 + last_row;  // last key any row of the tile sees
+  const int nchunks = kmax / KC + 1;
   const size_t row_stride = (size_t)a.n_kv * HD;
   const size_t cbase = (size_t)a.layer * a.max_seq * row_stride + (size_t)kvh * HD;
-  float* kw = ksh[wave];
-  float* vw = vsh[wave];
-  float* pw = psh[wave];
+  float* kw = lds + wave * SLAB;
+  float* pw = kw + KC * KS;
 
-  // A operand: row i = lane % 16 of the tile, dims 4s + lane / 16
   const int ai = lane & 15, ak = lane >> 4;
   const int aq = r0 + ai / GP, ag = ai % GP;
   const bool arow = aq < a.rows && ag < G;
-  const float* qp = a.q + (size_t)(arow ? aq : 0) * a.q_stride + (size_t)(kvh * G + (arow ? ag : 0)) * HD;
-  float qa[HD / 4];
+  const float* qp = a.q + (size_t)(arow ? aq : 0) * a.q_stride +
+                    (size_t)(kvh * G + (arow ? ag : 0)) * HD + ak * (HD / 4);
+  f4_t qa[HD / 16];
 #pragma unroll
-  for (int st = 0; st < HD / 4; ++st) qa[st] = arow ? qp[4 * st + ak] : 0.0f;
+  for (int s4 = 0; s4 < HD / 16; ++s4)
+    qa[s4] = arow ? *(const f4_t*)(qp + 4 * s4) : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // D-layout rows of this lane: 4 * (lane / 16) + i
   int dq[4], dpos[4];
@@ -768,43 +773,66 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto load_chunk = [&](int k0, f4_t* kr, f4_t* vr) {
-#pragma unroll
-    for (int u = 0; u < KF4; ++u) {
-      const int f = lane + 64 * u;       // float4 index in the chunk
-      const int key = f / (HD / 4);
-      const int c4 = f - key * (HD / 4);
-      const size_t off = cbase + (size_t)min(k0 + key, kmax) * row_stride + 4 * c4;
-      kr[u] = *(const f4_t*)(a.keys + off);
-      vr[u] = *(const f4_t*)(a.values + off);
-    }
-  };
-  f4_t kn[KF4], vn[KF4];
-  load_chunk(0, kn, vn);
-  for (int k0 = 0; k0 <= kmax; k0 += KC) {
-    // this chunk's rows to LDS, the next chunk's loads in flight
+  auto load_k = [&](int k0, f4_t* kr) {
 #pragma unroll
     for (int u = 0; u < KF4; ++u) {
       const int f = lane + 64 * u;
       const int key = f / (HD / 4);
       const int c4 = f - key * (HD / 4);
-      float* kd = kw + key * KS + 4 * c4;
-      kd[0] = kn[u].x;
-      kd[1] = kn[u].y;
-      kd[2] = kn[u].z;
-      kd[3] = kn[u].w;
-      *(f4_t*)(vw + key * HD + 4 * c4) = vn[u];
+      kr[u] = *(const f4_t*)(a.keys + cbase + (size_t)min(k0 + key, kmax) * row_stride + 4 * c4);
     }
-    if (k0 + KC <= kmax) load_chunk(k0 + KC, kn, vn);
+  };
+  // B operand of P V: V[k0 + 4 st + ak][16 t + lane % 16]
+  auto load_v = [&](int k0, float* vr) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        vr[t * 4 + st] = a.values[cbase + (size_t)min(k0 + 4 * st + ak, kmax) * row_stride +
+                                  16 * t + (lane & 15)];
+  };
+  f4_t kn[KF4];
+  float vn[VPRE ? NT * 4 : 1];
+  if (wave < nchunks) {
+    load_k(wave * KC, kn);
+    if constexpr (VPRE) load_v(wave * KC, vn);
+  }
+  for (int c = wave; c < nchunks; c += W) {
+    const int k0 = c * KC;
+#pragma unroll
+    for (int u = 0; u < KF4; ++u) {
+      const int f = lane + 64 * u;
+      const int key = f / (HD / 4);
+      const int c4 = f - key * (HD / 4);
+      *(f4_t*)(kw + key * KS + 4 * c4) = kn[u];
+    }
+    float vc[NT * 4];
+    if constexpr (VPRE) {
+#pragma unroll
+      for (int e = 0; e < NT * 4; ++e) vc[e] = vn[e];
+    }
+    if (c + W < nchunks) {
+      load_k(k0 + W * KC, kn);
+      if constexpr (VPRE) load_v(k0 + W * KC, vn);
+    }
+    if constexpr (!VPRE) load_v(k0, vc);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes landed
     __builtin_amdgcn_wave_barrier();
 
-    // S = Q K^T for keys k0 .. k0 + 15
-    f4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // S = Q K^T for keys k0 .. k0 + 15: four independent accumulator chains
+    f4_t sc4[4];
 #pragma unroll
-    for (int st = 0; st < HD / 4; ++st)
-      sacc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], kw[(lane & 15) * KS + 4 * st + ak],
-                                                  sacc, 0, 0, 0);
+    for (int q = 0; q < 4; ++q) sc4[q] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const float* krow = kw + (lane & 15) * KS + ak * (HD / 4);
+#pragma unroll
+    for (int s4 = 0; s4 < HD / 16; ++s4) {
+      const f4_t b4 = *(const f4_t*)(krow + 4 * s4);
+      sc4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s4].x, b4.x, sc4[0], 0, 0, 0);
+      sc4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s4].y, b4.y, sc4[1], 0, 0, 0);
+      sc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s4].z, b4.z, sc4[2], 0, 0, 0);
+      sc4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s4].w, b4.w, sc4[3], 0, 0, 0);
+    }
+    const f4_t sacc = (sc4[0] + sc4[1]) + (sc4[2] + sc4[3]);
     const int key = k0 + (lane & 15);
     float pr[4];
 #pragma unroll
@@ -833,18 +861,43 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int st = 0; st < 4; ++st)
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-            pa[st], vw[(4 * st + ak) * HD + 16 * t + (lane & 15)], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[st], vc[t * 4 + st], acc[t], 0, 0, 0);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // reads of this chunk done before the next writes
     __builtin_amdgcn_wave_barrier();
   }
+
+  // merge the W waves' partials of every row (wave order), then store
+  __syncthreads();  // every wave is done with its slab: the merge area reuses it
+  float* macc = lds;                       // [W][16][HD]
+  float* mml = lds + W * 16 * HD;          // [W][16] max, then [W][16] sum
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if (!dvalid[i]) continue;
     const int m = 4 * (lane >> 4) + i;
-    float* o = a.out + (size_t)dq[i] * a.out_stride + (size_t)(kvh * G + m % GP) * HD;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) o[16 * t + (lane & 15)] = acc[t][i] / lrow[i];
+    for (int t = 0; t < NT; ++t) macc[(wave * 16 + m) * HD + 16 * t + (lane & 15)] = acc[t][i];
+    if ((lane & 15) == 0) {
+      mml[wave * 16 + m] = mrow[i];
+      mml[W * 16 + wave * 16 + m] = lrow[i];
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 16 * HD; e += W * 64) {
+    const int m = e / HD;
+    const int d = e - m * HD;
+    const int qr = r0 + m / GP;
+    if (qr >= a.rows || (m % GP) >= G) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, mml[w * 16 + m]);
+    float lsum = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float mw = mml[w * 16 + m];
+      const float f = mw == -INFINITY ? 0.0f : expf(mw - mx);
+      lsum += mml[W * 16 + w * 16 + m] * f;
+      o += macc[(w * 16 + m) * HD + d] * f;
+    }
+    a.out[(size_t)qr * a.out_stride + (size_t)(kvh * G + m % GP) * HD + d] = o / lsum;
   }
 }
 
@@ -1240,10 +1293,9 @@ bool prefill_attention_supported(int hd, int group) {
 template <int HD, int GP>
 static void prefill_launch(const AttnArgs& a, hipStream_t stream) {
   constexpr int QT = 16 / GP;
-  constexpr int W = prefill_waves(HD);
   const int tiles = (a.rows + QT - 1) / QT;
-  hipLaunchKernelGGL((attn_prefill_kernel<HD, GP>), dim3((tiles + W - 1) / W, a.n_kv),
-                     dim3(W * 64), 0, stream, a);
+  hipLaunchKernelGGL((attn_prefill_kernel<HD, GP>), dim3(tiles, a.n_kv),
+                     dim3(prefill_waves(HD) * 64), 0, stream, a);
 }
 
 template <int HD>
