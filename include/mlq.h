@@ -250,6 +250,14 @@ int mlq_set_gemv_split(int split);
  * MLQ_ERR_INVALID_ARG outside 0..64. */
 int mlq_set_gemm_split(int split);
 
+/* Skinny GEMM (9..64 rows) plan override for tuning and tests
+ * (process-wide): `tiles` weight tiles of 16 rows per workgroup (1, 2 or 4)
+ * and `splits` K ranges per tile group (1..8; ranges beyond the number of
+ * 128-k groups are capped), whose fp32 partials the last workgroup to
+ * finish sums in range order; 0 leaves that choice to the planner. Query
+ * mlq_linear_workspace after changing it. MLQ_ERR_INVALID_ARG otherwise. */
+int mlq_set_skinny_plan(int tiles, int splits);
+
 /* Add bias[n] to every row of y[m, n] on the device (the reference adds the
  * bias on the host after download, src/cuda_quant.cu:229-235, 327-329). */
 int mlq_add_bias(float* y, const float* bias, int m, int n,

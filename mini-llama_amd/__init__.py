@@ -140,6 +140,7 @@ SIGNATURES = {
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
     "mlq_set_gemv_split": ([_I], _I),
     "mlq_set_gemm_split": ([_I], _I),
+    "mlq_set_skinny_plan": ([_I, _I], _I),
     "mlq_rmsnorm": ([_P, _P, _P, _I, _I, _F, _P], _I),
     "mlq_add": ([_P, _P, _P, _I64, _P], _I),
     "mlq_mul": ([_P, _P, _P, _I64, _P], _I),
@@ -515,6 +516,13 @@ def set_gemm_split(split: int = 0) -> None:
     K range; 0 = planner). Workspaces sized before the change may be too
     small afterwards: `linear` with workspace="auto" re-queries the size."""
     _check(lib().mlq_set_gemm_split(split), "mlq_set_gemm_split")
+
+
+def set_skinny_plan(tiles: int = 0, splits: int = 0) -> None:
+    """Override the skinny GEMM's weight tiles per workgroup (1, 2, 4) and K
+    ranges per tile group (1..8); 0 = planner. The workspace size may change
+    with it."""
+    _check(lib().mlq_set_skinny_plan(tiles, splits), "mlq_set_skinny_plan")
 
 
 def add_bias(y, bias, stream=None):

@@ -241,7 +241,7 @@ int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes) {
   if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
   *bytes = w->type == MLQ_F32 || uses_gemv(w, m) ? 0
-           : m <= kSkinnyMaxRows ? skinny_x_bytes(m, w->k)
+           : m <= kSkinnyMaxRows ? skinny_workspace_bytes(w->type, m, w->n, w->k)
                                  : gemm_workspace_bytes(m, w->n, w->k);
   return MLQ_OK;
 }
@@ -262,18 +262,13 @@ int mlq_linear_epi(const mlq_weight* w, const float* x, float* y, int m,
   if (w->type == MLQ_F32)
     return hip_status(launch_linear_f32((const float*)w->base, w->n, w->k, x, y, m, s, epi));
   if (uses_gemv(w, m)) return hip_status(launch_gemv(*w, x, y, m, s, epi));
-  const size_t need = m <= kSkinnyMaxRows ? skinny_x_bytes(m, w->k)
+  const size_t need = m <= kSkinnyMaxRows ? skinny_workspace_bytes(w->type, m, w->n, w->k)
                                            : gemm_workspace_bytes(m, w->n, w->k);
   if (workspace == nullptr || workspace_bytes < need)
     return MLQ_ERR_BUFFER_TOO_SMALL;
   if (((uintptr_t)workspace & 255u) != 0) return MLQ_ERR_INVALID_ARG;
-  if (m <= kSkinnyMaxRows) {
-    // batched decode: fragment-ordered fp16 copy of x, then the skinny GEMM
-    _Float16* xf = (_Float16*)workspace;
-    rc = hip_status(launch_x_to_frag(x, xf, m, w->k, s));
-    if (rc != MLQ_OK) return rc;
-    return hip_status(launch_skinny(*w, xf, y, m, s, epi));
-  }
+  if (m <= kSkinnyMaxRows)  // batched decode: fp16 x copy, skinny GEMM
+    return hip_status(launch_skinny_ws(*w, x, y, m, workspace, workspace_bytes, s, epi));
   return hip_status(launch_gemm_ws(*w, x, y, m, workspace, workspace_bytes, s, epi));
 }
 
@@ -322,6 +317,13 @@ int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,
 int mlq_set_gemm_split(int split) {
   if (split < 0 || split > 64) return MLQ_ERR_INVALID_ARG;
   set_gemm_split(split);
+  return MLQ_OK;
+}
+
+int mlq_set_skinny_plan(int tiles, int splits) {
+  const bool tiles_ok = tiles == 0 || tiles == 1 || tiles == 2 || tiles == 4;
+  if (!tiles_ok || splits < 0 || splits > 8) return MLQ_ERR_INVALID_ARG;
+  set_skinny_plan(tiles, splits);
   return MLQ_OK;
 }
 

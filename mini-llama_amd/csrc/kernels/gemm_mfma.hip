@@ -531,17 +531,14 @@ hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
-  const size_t outs = (size_t)a.m * a.ny;
-  if (a.n % 4 == 0) {
-    const size_t threads = outs / 4;
-    split_reduce_kernel<true><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
-        a.part, a.y, a.m, a.n, a.splits, a.epi, a.ny);
-  } else {
-    split_reduce_kernel<false><<<(unsigned)((outs + 255) / 256), 256, 0, stream>>>(
-        a.part, a.y, a.m, a.n, a.splits, a.epi, a.ny);
-  }
-  return hipGetLastError();
+  return launch_split_reduce(a.part, a.y, a.m, a.n, a.splits, a.epi, stream);
 }
+
+int g_split_override = 0;  // mlq_set_gemm_split; 0 = planner
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+}  // namespace
 
 // Compute units of the current device (256 on MI355X), read once.
 int device_cus() {
@@ -556,11 +553,20 @@ int device_cus() {
   return cus;
 }
 
-int g_split_override = 0;  // mlq_set_gemm_split; 0 = planner
-
-size_t align256(size_t b) { return (b + 255) / 256 * 256; }
-
-}  // namespace
+hipError_t launch_split_reduce(const float* part, float* y, int m, int n, int splits,
+                               const Epilogue& epi, hipStream_t stream) {
+  const int ny = epi.act == kEpiSwiGLU ? n / 2 : n;
+  const size_t outs = (size_t)m * ny;
+  if (n % 4 == 0) {
+    const size_t threads = outs / 4;
+    split_reduce_kernel<true><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
+        part, y, m, n, splits, epi, ny);
+  } else {
+    split_reduce_kernel<false><<<(unsigned)((outs + 255) / 256), 256, 0, stream>>>(
+        part, y, m, n, splits, epi, ny);
+  }
+  return hipGetLastError();
+}
 
 // Row stride (halves) of the fp16 activation copy: whole 128-k groups, so
 // every stage (GEMM) and group (skinny GEMM) of a row stays inside it.

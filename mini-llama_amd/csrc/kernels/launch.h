@@ -73,14 +73,27 @@ int f16_row_stride(int k);
 hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,
                            hipStream_t stream);
 
-// skinny.hip: 9..64 rows of x from its fragment-ordered fp16 copy
-// (skinny_x_bytes(m, k) bytes, made by launch_x_to_frag).
+// Compute units of the current device (256 on MI355X), read once.
+int device_cus();
+// y = epilogue(sum over s of part[s] in order), part [splits][m][n] fp32
+// (split-K partial slices of the prefill and skinny GEMMs).
+hipError_t launch_split_reduce(const float* part, float* y, int m, int n, int splits,
+                               const Epilogue& epi, hipStream_t stream);
+
+// skinny.hip: 9..64 rows of x. launch_skinny_ws makes the fragment-ordered
+// fp16 copy of x in ws, then runs the skinny GEMM (K split over
+// workgroups when the planner chooses it: counters and partial slices
+// after the copy); ws holds skinny_workspace_bytes(type, m, n, k) bytes,
+// 256-byte aligned.
 constexpr int kSkinnyMaxRows = 64;
 size_t skinny_x_bytes(int m, int k);
-hipError_t launch_x_to_frag(const float* x, _Float16* xf, int m, int k,
-                            hipStream_t stream);
-hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int m,
-                         hipStream_t stream, const Epilogue& epi = Epilogue());
+size_t skinny_workspace_bytes(int type, int m, int n, int k);
+hipError_t launch_skinny_ws(const mlq_weight& w, const float* x, float* y, int m,
+                            void* ws, size_t ws_bytes, hipStream_t stream,
+                            const Epilogue& epi = Epilogue());
+// Plan override (0 = planner): weight tiles per workgroup (1, 2, 4) and K
+// ranges per tile group (1..8); validated by the caller.
+void set_skinny_plan(int tiles, int splits);
 
 // linear_f32.hip: fp32 W [n][k], any m (passes of up to 8 rows).
 hipError_t launch_linear_f32(const float* w, int n, int k, const float* x, float* y, int m,

@@ -23,7 +23,19 @@
 //  - Group g+1's weight lines and x fragments are requested before group
 //    g's MFMAs run. K slices combine through LDS in slice order, one tile
 //    at a time.
+//  - Every workgroup needs the x fragments of its whole K range, so with
+//    one K range per tile group each CU reads all of x (512 KiB at m = 64,
+//    K = 4096; 2.4 MiB at K = 18944: that read, not the weights, bounds the
+//    kernel). The K range can be split over S workgroups (S = 2..8): each
+//    reads 1/S of x and writes fp32 partial outputs to the workspace, and
+//    the prefill GEMM's reduce kernel sums the S slices in order and
+//    applies the epilogue (deterministic). Handing the partials to the last
+//    workgroup to finish inside the kernel instead (atomic count + device
+//    fences) measured 10-20x slower on MI355X: a device-scope release
+//    writes back the XCD's L2 and the acquire invalidates it.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "../mlq_layout.h"
 #include "device_common.h"
@@ -44,6 +56,8 @@ struct SkinnyArgs {
   int m, n, g, nt;
   Epilogue epi;
   int ny;              // output columns: n, or n/2 under kEpiSwiGLU
+  int splits;          // K ranges per tile group (workgroups per tile group)
+  float* part;         // splits > 1: partial outputs [splits][m][n]
 };
 
 // One 128-k group of T weight tiles and the x fragments of all row blocks.
@@ -132,10 +146,16 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int t0 = blockIdx.x * T;
-  const int gw = (a.g + kWaves - 1) / kWaves;
-  const int g0 = wave * gw;
-  const int ng = max(0, min(gw, a.g - g0));
+  // consecutive workgroups take consecutive K ranges of one tile group
+  // (hardware places workgroup b on XCD b % 8, so with S | 8 each XCD's
+  // L2 holds the x fragments of one K range only)
+  const int sp = blockIdx.x % a.splits;
+  const int tg = blockIdx.x / a.splits;
+  const int t0 = tg * T;
+  const int kg0 = sp * a.g / a.splits, kg1 = (sp + 1) * a.g / a.splits;
+  const int gw = (kg1 - kg0 + kWaves - 1) / kWaves;
+  const int g0 = kg0 + wave * gw;
+  const int ng = max(0, min(gw, kg1 - g0));
 
   constexpr uint32_t QB = QT == MLQ_Q8_0 ? 2048u : 1024u;
   rsrc_t rq[T], rd[T], rm[T];
@@ -186,6 +206,27 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyArgs a) {
   // + i, weight row lane%16 of tile t. K slices combine in slice order, one
   // tile at a time.
   const int col = lane & 15, rq4 = 4 * (lane >> 4);
+  const bool split = a.splits > 1;
+  // outputs of tile t from `sum` (K slices of the workgroup): the epilogue
+  // into y
+  auto store = [&](auto sum, int t) {
+    if (a.epi.act == kEpiSwiGLU) {
+      for (int o = tid; o < a.m * 8; o += kThreads) {
+        const int r = o / 8, c = o % 8;
+        const int row = (t0 + t) * kTileRows + c;
+        if (row >= a.n) continue;
+        const float g = add_bias(a.epi, sum(r, c, row), row);
+        const float u = add_bias(a.epi, sum(r, c + 8, row + 8), row + 8);
+        a.y[(size_t)r * a.ny + glu_col(row)] = silu_f(g) * u;
+      }
+    } else {
+      for (int o = tid; o < a.m * 16; o += kThreads) {
+        const int r = o / 16, c = o % 16;
+        const int row = (t0 + t) * kTileRows + c;
+        if (row < a.n) a.y[(size_t)r * a.n + row] = add_bias(a.epi, sum(r, c, row), row);
+      }
+    }
+  };
 #pragma unroll
   for (int t = 0; t < T; ++t) {
 #pragma unroll
@@ -194,26 +235,21 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyArgs a) {
       for (int i = 0; i < 4; ++i)
         part[(wave * 64 + 16 * mb + rq4 + i) * 16 + col] = acc[t][mb][i];
     __syncthreads();
-    auto wave_sum = [&](int r, int c) {
+    auto slice_sum = [&](int r, int c, int) {
       float s = 0.0f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) s += part[(w * 64 + r) * 16 + c];
       return s;
     };
-    if (a.epi.act == kEpiSwiGLU) {
-      for (int o = tid; o < a.m * 8; o += kThreads) {
-        const int r = o / 8, c = o % 8;
-        const int row = (t0 + t) * kTileRows + c;
-        if (row >= a.n) continue;
-        const float g = add_bias(a.epi, wave_sum(r, c), row);
-        const float u = add_bias(a.epi, wave_sum(r, c + 8), row + 8);
-        a.y[(size_t)r * a.ny + glu_col(row)] = silu_f(g) * u;
-      }
+    if (!split) {
+      store(slice_sum, t);
     } else {
+      // this K range's partial outputs (no epilogue)
+      float* out = a.part + (size_t)sp * a.m * a.n;
       for (int o = tid; o < a.m * 16; o += kThreads) {
         const int r = o / 16, c = o % 16;
         const int row = (t0 + t) * kTileRows + c;
-        if (row < a.n) a.y[(size_t)r * a.n + row] = add_bias(a.epi, wave_sum(r, c), row);
+        if (row < a.n) out[(size_t)r * a.n + row] = slice_sum(r, c, row);
       }
     }
     if (t + 1 < T) __syncthreads();
@@ -251,19 +287,59 @@ __global__ __launch_bounds__(256) void x_to_frag_kernel(const float* x, _Float16
   *(uint4*)(xf + ((((size_t)j * mbt + mb) * 4 + b) * 64 + lane) * 8) = o;
 }
 
-// Weight tiles per workgroup: reuse each x fragment for up to four tiles
-// while at least 256 workgroups remain (measured: T = 4 at N = 18944, 2 at
-// N = 11008, 1 at N = 4096).
-int tiles_per_group(int nt) {
-  if (nt / 4 >= 256) return 4;
-  if (nt / 2 >= 256) return 2;
-  return 1;
+int g_tiles_override = 0;   // mlq_set_skinny_plan; 0 = planner
+int g_splits_override = 0;
+
+struct SkinnyPlan {
+  int tiles, splits;
+};
+
+// Weight tiles per workgroup (T) and K ranges per tile group (S). A
+// workgroup reads its K range of x once for all of its T tiles, so per CU
+// the x bytes are m_pad * (K / S) * 2 and the weight bytes T * 16 * (K / S)
+// * (bytes per weight); more of either per workgroup means fewer
+// workgroups. Cost model (us per round of workgroups on the chip): x at
+// ~110 GB/s per CU from L2, weights at ~20 GB/s per CU (HBM shared by all
+// CUs), the larger of the two, plus ~1.5 us per round; S > 1 adds the
+// reduce launch (~2 us) and the partial slices (written, read, and y
+// written: (2S + 1) m n 4 bytes at ~4 TB/s).
+SkinnyPlan skinny_plan(int type, int m, int n, int k) {
+  const Geometry geo = geometry(n, k);
+  const int cus = device_cus();
+  const double mpad = (double)((m + 15) / 16 * 16);
+  const double bpw = type == MLQ_Q8_0 ? 34.0 / 32 : type == MLQ_Q4_1 ? 20.0 / 32 : 18.0 / 32;
+  SkinnyPlan best{1, 1};
+  double best_t = 0.0;
+  bool have = false;
+  for (int t : {1, 2, 4}) {
+    if (g_tiles_override > 0 && t != g_tiles_override) continue;
+    // four tiles of 64 rows spill registers for q8_0 / q4_1 (planner only)
+    if (g_tiles_override == 0 && t == 4 && m > 48 && type != MLQ_Q4_0) continue;
+    for (int sp : {1, 2, 4, 8, 0}) {
+      // candidates 1, 2, 4, 8 within the group count, or the override alone
+      if ((g_splits_override > 0) != (sp == 0) || sp > geo.g) continue;
+      const int s_eff = sp == 0 ? std::min(g_splits_override, geo.g) : sp;
+      const int wgs = (geo.nt + t - 1) / t * s_eff;
+      const int rounds = (wgs + cus - 1) / cus;
+      const double kr = (double)geo.g * kGroupK / s_eff;  // k per workgroup
+      const double x_us = mpad * kr * 2.0 / 110e3;
+      const double w_us = t * 16.0 * kr * bpw / 20e3;
+      double cost = rounds * (std::max(x_us, w_us) + 1.5);
+      if (s_eff > 1) cost += 2.0 + (2.0 * s_eff + 1.0) * m * (double)n * 4.0 / 4e6;
+      if (!have || cost < best_t) {
+        best = SkinnyPlan{t, s_eff};
+        best_t = cost;
+        have = true;
+      }
+    }
+  }
+  return best;
 }
 
 template <int QT, int T>
 hipError_t launch_t(const SkinnyArgs& a, hipStream_t stream) {
   const int mb = (a.m + 15) / 16;
-  const unsigned grid = (unsigned)((a.nt + T - 1) / T);
+  const unsigned grid = (unsigned)((a.nt + T - 1) / T * a.splits);
   switch (mb) {
     case 1: skinny_kernel<QT, 1, T><<<grid, kThreads, 0, stream>>>(a); break;
     case 2: skinny_kernel<QT, 2, T><<<grid, kThreads, 0, stream>>>(a); break;
@@ -274,13 +350,15 @@ hipError_t launch_t(const SkinnyArgs& a, hipStream_t stream) {
 }
 
 template <int QT>
-hipError_t launch_typed(const SkinnyArgs& a, hipStream_t stream) {
-  switch (tiles_per_group(a.nt)) {
+hipError_t launch_typed(const SkinnyArgs& a, int tiles, hipStream_t stream) {
+  switch (tiles) {
     case 1: return launch_t<QT, 1>(a, stream);
     case 2: return launch_t<QT, 2>(a, stream);
     default: return launch_t<QT, 4>(a, stream);
   }
 }
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 }  // namespace
 
@@ -289,26 +367,34 @@ size_t skinny_x_bytes(int m, int k) {
   return (size_t)(m + 15) / 16 * 16 * kp * 2;
 }
 
-hipError_t launch_x_to_frag(const float* x, _Float16* xf, int m, int k,
-                            hipStream_t stream) {
-  const int kp = (k + kGroupK - 1) / kGroupK * kGroupK;
-  const int mbt = (m + 15) / 16;
-  const size_t items = (size_t)mbt * 16 * (kp / 8);
-  x_to_frag_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(x, xf, m, k, kp, mbt);
-  return hipGetLastError();
+void set_skinny_plan(int tiles, int splits) {
+  g_tiles_override = tiles;
+  g_splits_override = splits;
 }
 
-hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int m,
-                         hipStream_t stream, const Epilogue& epi) {
+// x copy, then (split K) the partial slices.
+size_t skinny_workspace_bytes(int type, int m, int n, int k) {
+  const SkinnyPlan p = skinny_plan(type, m, n, k);
+  size_t b = align256(skinny_x_bytes(m, k));
+  if (p.splits > 1) b += (size_t)p.splits * m * n * 4;
+  return b;
+}
+
+hipError_t launch_skinny_ws(const mlq_weight& w, const float* x, float* y, int m,
+                            void* ws, size_t ws_bytes, hipStream_t stream,
+                            const Epilogue& epi) {
   if (m < 1 || m > kSkinnyMaxRows) return hipErrorInvalidValue;
   // 32-bit buffer offsets for the x fragments of a wave
   if (skinny_x_bytes(m, w.k) >= (1ull << 31)) return hipErrorInvalidValue;
+  if (ws == nullptr || ws_bytes < skinny_workspace_bytes(w.type, m, w.n, w.k))
+    return hipErrorInvalidValue;
   const Geometry geo = geometry(w.n, w.k);
+  const SkinnyPlan p = skinny_plan(w.type, m, w.n, w.k);
   SkinnyArgs a;
   a.qs = (const uint8_t*)w.base + w.qs_off;
   a.d = (const uint8_t*)w.base + w.d_off;
   a.mn = w.type == MLQ_Q4_1 ? (const uint8_t*)w.base + w.m_off : nullptr;
-  a.xf = xf;
+  a.xf = (const _Float16*)ws;
   a.y = y;
   a.m = m;
   a.n = w.n;
@@ -316,11 +402,26 @@ hipError_t launch_skinny(const mlq_weight& w, const _Float16* xf, float* y, int 
   a.nt = geo.nt;
   a.epi = epi;
   a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
+  a.splits = p.splits;
+  a.part = p.splits > 1
+      ? (float*)((uint8_t*)ws + align256(skinny_x_bytes(m, w.k)))
+      : nullptr;
+  // fragment-ordered fp16 copy of x
+  const int kp = (w.k + kGroupK - 1) / kGroupK * kGroupK;
+  const int mbt = (m + 15) / 16;
+  const size_t items = (size_t)mbt * 16 * (kp / 8);
+  x_to_frag_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(
+      x, (_Float16*)ws, m, w.k, kp, mbt);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   switch (w.type) {
-    case MLQ_Q8_0: return launch_typed<MLQ_Q8_0>(a, stream);
-    case MLQ_Q4_0: return launch_typed<MLQ_Q4_0>(a, stream);
-    default: return launch_typed<MLQ_Q4_1>(a, stream);
+    case MLQ_Q8_0: e = launch_typed<MLQ_Q8_0>(a, p.tiles, stream); break;
+    case MLQ_Q4_0: e = launch_typed<MLQ_Q4_0>(a, p.tiles, stream); break;
+    default: e = launch_typed<MLQ_Q4_1>(a, p.tiles, stream); break;
   }
+  if (e != hipSuccess || p.splits == 1) return e;
+  // the K ranges' partial slices, summed in order, then the epilogue
+  return launch_split_reduce(a.part, y, m, w.n, p.splits, epi, stream);
 }
 
 }  // namespace mlq

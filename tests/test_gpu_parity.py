@@ -300,6 +300,75 @@ def test_gemm_every_split(pkg, oracle, cuda, qtype, split):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("tiles,splits", [(1, 2), (2, 3), (4, 4), (1, 8), (2, 1)])
+def test_skinny_split_k(pkg, oracle, cuda, qtype, tiles, splits):
+    """Skinny GEMM (9..64 rows) with its K range split over workgroups whose
+    partial slices a reduce pass sums in range order. Ragged shapes (rows
+    past m, tile groups past n, k tails, more ranges than 128-k groups);
+    the stated bar against the oracle, agreement with the unsplit kernel to
+    fp32 summation order, repeat calls and graph replays bit-identical,
+    bias and SwiGLU epilogues applied once after the sum."""
+    torch = _torch()
+    _print_case(test="skinny_split", qtype=qtype, tiles=tiles, splits=splits)
+    try:
+        for m, n, k in [(9, 40, 200), (33, 48, 1001), (64, 256, 4096),
+                        (50, 17, 4000), (16, 8200, 256), (61, 1040, 3000)]:
+            blocks = make_blocks(qtype, n, k, seed=5 * n + k + m)
+            x = make_x(m, k, seed=k + 13)
+            tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+            xd = _dev(x, cuda)
+            ref = oracle.linear(x, blocks, (n, k), qtype, threads=8)
+            atol = 1e-3 * np.linalg.norm(x, axis=1, keepdims=True) * np.sqrt(k / 4096)
+            pkg.set_skinny_plan(1, 1)
+            one = pkg.linear(tw, xd, workspace=torch.empty(
+                pkg.workspace_bytes(tw, m), dtype=torch.uint8, device=cuda)).cpu().numpy()
+            pkg.set_skinny_plan(tiles, splits)
+            need = pkg.workspace_bytes(tw, m)
+            ranges = min(splits, -(-k // 128))
+            if ranges > 1:
+                assert need >= ranges * m * n * 4
+            ws = torch.empty(need, dtype=torch.uint8, device=cuda)
+            got = pkg.linear(tw, xd, workspace=ws).cpu().numpy()
+            assert tolerance_ok(got, ref, x, k).all(), (m, n, k, error_report(got, ref, x, k))
+            assert np.all(np.abs(got - one) <= 1e-3 * atol), (m, n, k)
+            again = pkg.linear(tw, xd, workspace=ws).cpu().numpy()
+            assert np.array_equal(got, again), (m, n, k)
+            bias = torch.from_numpy(make_x(1, n, seed=n + 3)[0]).to(cuda)
+            plain = pkg.linear(tw, xd, workspace=ws)
+            assert torch.equal(pkg.linear(tw, xd, workspace=ws, bias=bias), plain + bias)
+            if n % 16 == 0:
+                glu = pkg.linear(tw, xd, workspace=ws, bias=bias,
+                                 act=pkg.EPI_SWIGLU).cpu().numpy()
+                pb = (plain + bias).cpu().numpy().astype(np.float64)
+                rows = np.arange(n // 2)
+                want = (_silu64(pb[:, 16 * (rows // 8) + rows % 8])
+                        * pb[:, 16 * (rows // 8) + 8 + rows % 8])
+                assert np.abs(glu - want).max() <= 1e-5 * (np.abs(want).max() + 1e-30)
+        # captured in a graph: every replay (with eager work between them)
+        # equals the eager result
+        y = torch.empty((m, n), dtype=torch.float32, device=cuda)
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            pkg.linear(tw, xd, y=y, workspace=ws)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            pkg.linear(tw, xd, y=y, workspace=ws)
+        for _ in range(3):
+            y.zero_()
+            pkg.linear(tw, xd, workspace=ws)  # eager call on the same workspace
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy(), got)
+    finally:
+        pkg.set_skinny_plan(0, 0)
+
+
+def _silu64(g):
+    return g / (1.0 + np.exp(-g))
+
+
+@pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("m,n,k", [(1, 48, 128), (1, 300, 1001), (4, 64, 512),
                                    (16, 8200, 256), (40, 100, 300), (130, 70, 300),
                                    (300, 272, 640), (512, 2048, 256)])
@@ -317,10 +386,6 @@ def test_fused_bias_matches_separate_add(pkg, cuda, qtype, m, n, k):
     plain = pkg.linear(tw, xd)
     fused = pkg.linear(tw, xd, bias=bias)
     assert torch.equal(fused, plain + bias)
-
-
-def _silu64(g):
-    return g / (1.0 + np.exp(-g))
 
 
 @pytest.mark.parametrize("qtype", TYPES)
