@@ -245,14 +245,18 @@ __device__ __forceinline__ h8_t decode_w(const WStage<QT>& st, int j, int ks) {
 template <int N>
 struct Slot { static constexpr int v = N; };
 
-// OCC: workgroups per CU the register budget is sized for. q4_0 with the
-// fp16 copy of x fits the whole pipeline in 256 registers a lane, so two
-// workgroups share a CU and each hides the other's decode and LDS latency
-// (measured 5-12 % faster on 512-2048-row shapes); q8_0 and q4_1 carry
-// more weight registers per stage and keep one workgroup per CU (a
-// pipeline cut to two weight stages to fit measured slower).
-template <int QT, int XM, int OCC = 1>
+// OCC: workgroups per CU the register budget is sized for; XS: activation
+// register slots. q4_0 with the fp16 copy of x fits the whole pipeline in
+// 256 registers a lane, so two workgroups share a CU and each hides the
+// other's decode and LDS latency (measured 5-12 % faster on 512-2048-row
+// shapes, neutral on small grids). q8_0 and q4_1 carry more weight
+// registers per stage: they fit two per CU with one activation slot (x of
+// stage s+2 requested in k step 0 of stage s, stored in its last), which
+// wins only when the grid has more workgroups than CUs (3-8 %; 2-8 % slower
+// on smaller grids), so the launcher picks it by grid size.
+template <int QT, int XM, int OCC = 1, int XS = 2>
 __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
+  constexpr int kXS = XS;  // activation register slots (1 or 2)
   __shared__ __align__(16) _Float16 as_buf[3][kBM * kStride];
 
   const int tid = threadIdx.x;
@@ -315,17 +319,26 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
       af[i] = *(const h8_t*)(as + (32 * i + fr) * kStride + 16 * ks + fk);
   };
 
-  // prologue: slabs 0 and 1 hold x(0), x(1); x(2) in register slot 0;
-  // W(0), W(1) in slots 0 and 1
-  XStage xs[2];
+  // prologue: slabs 0 and 1 hold x(0), x(1); W(0), W(1) in slots 0 and 1;
+  // with two x slots x(2) waits in slot 0
+  XStage xs[kXS];
   WStage<QT> ws[3];
-  lx(xs[0], 0);
-  lw(ws[0], 0);
-  lx(xs[1], 1);
-  lw(ws[1], 1);
-  sx(xs[0], 0, 0);
-  sx(xs[1], 1, 1);
-  lx(xs[0], min(2, last));
+  if constexpr (kXS == 2) {
+    lx(xs[0], 0);
+    lw(ws[0], 0);
+    lx(xs[1], 1);
+    lw(ws[1], 1);
+    sx(xs[0], 0, 0);
+    sx(xs[1], 1, 1);
+    lx(xs[0], min(2, last));
+  } else {
+    lx(xs[0], 0);
+    lw(ws[0], 0);
+    lw(ws[1], 1);
+    sx(xs[0], 0, 0);
+    lx(xs[0], 1);
+    sx(xs[0], 1, 1);
+  }
   __syncthreads();
 
   h8_t af[4], bf[2];
@@ -335,16 +348,18 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
 
   // Stage s; the register slots are compile-time (S = s mod 6): weights of
   // stage s in slot s%3 (s+1 in flight in (s+1)%3, s+2 requested into
-  // (s+2)%3), x(s+2) in slot s%2 (x(s+3) requested into (s+1)%2). Loads
-  // past the last stage re-read the last one, so the ring never branches.
+  // (s+2)%3 in k step 1). Two x slots: x(s+2) in slot s%2, x(s+3) requested
+  // into (s+1)%2 in k step 0; one slot: x(s+2) requested in k step 0 and
+  // stored in the last. Loads past the last stage re-read the last one, so
+  // the ring never branches.
   auto step = [&](int s, auto slot) {
     constexpr int S = decltype(slot)::v;
     constexpr int WC = S % 3, WN = (S + 1) % 3, WA = (S + 2) % 3;
-    constexpr int XC = S % 2, XA = (S + 1) % 2;
+    constexpr int XC = S % kXS, XA = (S + 1) % kXS;
     constexpr int BC = S % 3, BN = (S + 1) % 3, BA = (S + 2) % 3;
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      if (ks == 0) lx(xs[XA], min(s + 3, last));
+      if (ks == 0) lx(xs[XA], min(s + kXS + 1, last));
       if (ks == 1) lw(ws[WA], min(s + 2, last));
       h8_t an[4], bn[2];
       if (ks < kBK / 16 - 1) {
@@ -537,6 +552,8 @@ hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
     default:
       if constexpr (QT == MLQ_Q4_0)
         gemm_kernel<QT, kXF16, 2><<<grid, kThreads, 0, stream>>>(a);
+      else if ((int)grid > device_cus())  // a second workgroup per CU to run
+        gemm_kernel<QT, kXF16, 2, 1><<<grid, kThreads, 0, stream>>>(a);
       else
         gemm_kernel<QT, kXF16><<<grid, kThreads, 0, stream>>>(a);
       break;

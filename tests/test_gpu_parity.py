@@ -219,11 +219,12 @@ def test_linear_1d_input_and_aos_path(pkg, oracle, cuda, qtype):
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("m,n,k", [(9, 40, 200), (130, 70, 300), (64, 256, 4096),
                                    (300, 100, 1001), (33, 48, 1001), (50, 17, 4000),
-                                   (16, 8200, 256), (61, 16400, 300)])
+                                   (16, 8200, 256), (61, 16400, 300), (1030, 8200, 256)])
 def test_gemm_workspace_path_matches_direct(pkg, cuda, qtype, m, n, k):
     """mlq_linear_ws (fp16 copy of x made by a pre-pass) and the direct GEMM
     (x converted inside) round x to fp16 identically, so they must agree bit
-    for bit; the workspace contract is enforced."""
+    for bit (also when the grid exceeds the CU count and the workspace path
+    runs two workgroups per CU); the workspace contract is enforced."""
     torch = _torch()
     _print_case(test="gemm_ws", qtype=qtype, m=m, n=n, k=k)
     blocks = make_blocks(qtype, n, k, seed=m + n + k)
