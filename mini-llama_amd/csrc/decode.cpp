@@ -153,6 +153,10 @@ struct PrefillBuffers {
   float* apart;     // attention partials for kPrefillAttnRows rows
   void* lin;        // Linear workspace for n rows (and 1 row)
   size_t lin_bytes;
+  // n > kSkinnyMaxRows (prefill GEMM): fp16 GEMM inputs written by their
+  // producers (RMSNorm rows, the gate|up SwiGLU epilogue)
+  _Float16* xh;     // [n][f16_row_stride(dim)]
+  _Float16* gh;     // [n][f16_row_stride(hidden)]
   size_t total;
 };
 
@@ -205,6 +209,9 @@ int plan_prefill(const mlq_model* m, int n, char* base, PrefillBuffers* b) {
                                                     std::min(n, kPrefillAttnRows)));
   b->lin_bytes = lin;
   b->lin = take(lin);
+  const bool gemm_rows = n > kSkinnyMaxRows;
+  b->xh = gemm_rows ? (_Float16*)take(rows * f16_row_stride(dim) * 2) : nullptr;
+  b->gh = gemm_rows ? (_Float16*)take(rows * f16_row_stride(hid) * 2) : nullptr;
   b->total = off;
   return MLQ_OK;
 }
@@ -530,6 +537,26 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
                     int act) {
     return mlq_linear_epi(&w, x, y, rows, bias, act, b.lin, b.lin_bytes, stream);
   };
+  // Prefill GEMM rows (n > 64, quantized weights): the producers write the
+  // GEMMs' fp16 inputs directly (RMSNorm rows, the SwiGLU epilogue) and the
+  // o / down projections add the residual in their epilogue, which removes
+  // four fp16 copy passes and two residual passes per layer with the same
+  // roundings and additions.
+  auto gemm_rows = [&](const mlq_weight& w) { return n > kSkinnyMaxRows && w.type != MLQ_F32; };
+  auto f16_norm_ok = [&](const float* norm) {
+    return dim % 4 == 0 && ((uintptr_t)norm & 15) == 0 && dim <= 16 * 4 * 256;
+  };
+  // (xh rows are f16_row_stride(w.k) halves: w.k is dim or hidden, checked
+  // by plan())
+  auto gemm_f16 = [&](const mlq_weight& w, const _Float16* xh, float* y, const Epilogue& e) {
+    return hip(launch_gemm_f16(w, xh, y, n, b.lin, b.lin_bytes, s, e));
+  };
+  const int ldx = f16_row_stride(dim), ldh = f16_row_stride(hid);
+  if (n > kSkinnyMaxRows && ldh > hid) {
+    // the SwiGLU epilogue writes hidden columns only; the GEMM reading them
+    // needs zeros up to the padded row length
+    if ((rc = hip(launch_fill_zero(b.gh, (size_t)n * ldh * 2, s))) != MLQ_OK) return rc;
+  }
   if ((rc = hip(hipMemcpyAsync(b.tokens, tokens, (size_t)n * sizeof(int32_t),
                                hipMemcpyHostToDevice, s))) != MLQ_OK)
     return rc;
@@ -537,19 +564,30 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
     return rc;
   for (int li = 0; li < m->n_layers; ++li) {
     const mlq_layer& l = m->layers[li];
-    if ((rc = hip(launch_rmsnorm(b.x, l.attn_norm, b.h, n, dim, m->rms_norm_eps, s))) != MLQ_OK)
-      return rc;
     RopeRows rr;
+    const bool qkv_f16 = gemm_rows(l.wq) && (qkv_fused(l) || (gemm_rows(l.wk) && gemm_rows(l.wv))) &&
+                         f16_norm_ok(l.attn_norm);
+    auto proj = [&](const mlq_weight& w, float* y, const float* bias) {
+      if (!qkv_f16) return linear(w, b.h, y, n, bias, MLQ_EPI_NONE);
+      Epilogue e;
+      e.bias = bias;
+      return gemm_f16(w, b.xh, y, e);
+    };
+    if (qkv_f16)
+      rc = hip(launch_rmsnorm_f16(b.x, l.attn_norm, b.xh, n, dim, ldx, m->rms_norm_eps, s));
+    else
+      rc = hip(launch_rmsnorm(b.x, l.attn_norm, b.h, n, dim, m->rms_norm_eps, s));
+    if (rc != MLQ_OK) return rc;
     if (qkv_fused(l)) {
-      if ((rc = linear(l.wq, b.h, b.qkv, n, l.bq, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = proj(l.wq, b.qkv, l.bq)) != MLQ_OK) return rc;
       rr.q = b.qkv;
       rr.k = b.qkv + qd;
       rr.v = b.qkv + qd + kvd;
       rr.q_stride = rr.k_stride = rr.v_stride = qd + 2 * kvd;
     } else {
-      if ((rc = linear(l.wq, b.h, b.qkv, n, l.bq, MLQ_EPI_NONE)) != MLQ_OK) return rc;
-      if ((rc = linear(l.wk, b.h, b.k, n, l.bk, MLQ_EPI_NONE)) != MLQ_OK) return rc;
-      if ((rc = linear(l.wv, b.h, b.v, n, l.bv, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = proj(l.wq, b.qkv, l.bq)) != MLQ_OK) return rc;
+      if ((rc = proj(l.wk, b.k, l.bk)) != MLQ_OK) return rc;
+      if ((rc = proj(l.wv, b.v, l.bv)) != MLQ_OK) return rc;
       rr.q = b.qkv;
       rr.k = b.k;
       rr.v = b.v;
@@ -610,10 +648,35 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
       a.out_stride = qd;
       if ((rc = hip(launch_attention(a, s))) != MLQ_OK) return rc;
     }
-    // x2 = x + wo . attn (per-row residual: a separate add)
-    if ((rc = linear(l.wo, b.attn, b.x2, n, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
-    if ((rc = hip(launch_eltwise(kEltAdd, b.x, b.x2, b.x2, (int64_t)n * dim, s))) != MLQ_OK)
-      return rc;
+    // x2 = x + wo . attn (the GEMM adds the residual row by row)
+    if (gemm_rows(l.wo)) {
+      Epilogue e;
+      e.residual = b.x;
+      if ((rc = hip(launch_gemm_ws(l.wo, b.attn, b.x2, n, b.lin, b.lin_bytes, s, e))) != MLQ_OK)
+        return rc;
+    } else {
+      if ((rc = linear(l.wo, b.attn, b.x2, n, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+      if ((rc = hip(launch_eltwise(kEltAdd, b.x, b.x2, b.x2, (int64_t)n * dim, s))) != MLQ_OK)
+        return rc;
+    }
+    // x = x2 + w_down . swiglu(w_gate . h, w_up . h); with gate|up
+    // interleaved and prefill GEMM rows: fp16 input from RMSNorm, fp16
+    // SwiGLU output from the epilogue, residual in the down GEMM
+    if (glu_fused(l) && gemm_rows(l.w_gate) && gemm_rows(l.w_down) &&
+        f16_norm_ok(l.ffn_norm)) {
+      if ((rc = hip(launch_rmsnorm_f16(b.x2, l.ffn_norm, b.xh, n, dim, ldx, m->rms_norm_eps,
+                                       s))) != MLQ_OK)
+        return rc;
+      Epilogue eg;
+      eg.act = kEpiSwiGLU;
+      eg.yh = b.gh;
+      eg.yh_ld = ldh;
+      if ((rc = gemm_f16(l.w_gate, b.xh, nullptr, eg)) != MLQ_OK) return rc;
+      Epilogue ed;
+      ed.residual = b.x2;
+      if ((rc = gemm_f16(l.w_down, b.gh, b.x, ed)) != MLQ_OK) return rc;
+      continue;
+    }
     if ((rc = hip(launch_rmsnorm(b.x2, l.ffn_norm, b.h, n, dim, m->rms_norm_eps, s))) != MLQ_OK)
       return rc;
     if (glu_fused(l)) {

@@ -10,6 +10,8 @@
 // past the live length exit at once.
 #include <hip/hip_runtime.h>
 #include <math.h>
+
+#include <algorithm>
 #include <stdint.h>
 
 #include "device_common.h"
@@ -1088,9 +1090,82 @@ __global__ __launch_bounds__(kArgmaxSliceThreads) void argmax_final_kernel(
   }
 }
 
+// rmsnorm_vec_kernel with fp16 output rows of ld halves (zero past dim).
+template <int R>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_f16_kernel(
+    const float* __restrict__ x, const float* __restrict__ w,
+    _Float16* __restrict__ yh, int dim, int ld, float eps) {
+  __shared__ float part[kNormThreads / 64];
+  const int n4 = dim >> 2;
+  const f4_t* xr = (const f4_t*)(x + (size_t)blockIdx.x * dim);
+  uint2* yr = (uint2*)(yh + (size_t)blockIdx.x * ld);
+  const f4_t* w4 = (const f4_t*)w;
+  f4_t v[R], wv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = threadIdx.x + r * kNormThreads;
+    v[r] = i < n4 ? xr[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    wv[r] = i < n4 ? w4[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    ss += v[r].x * v[r].x;
+    ss += v[r].y * v[r].y;
+    ss += v[r].z * v[r].z;
+    ss += v[r].w * v[r].w;
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) total += part[i];
+  const float scale = sqrtf(total / (float)dim + eps);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = threadIdx.x + r * kNormThreads;
+    if (i < n4) {
+      uint2 o;
+      o.x = pack_h2(v[r].x * wv[r].x / scale, v[r].y * wv[r].y / scale);
+      o.y = pack_h2(v[r].z * wv[r].z / scale, v[r].w * wv[r].w / scale);
+      yr[i] = o;
+    }
+  }
+  for (int i = n4 + threadIdx.x; i < (ld >> 2); i += kNormThreads) yr[i] = make_uint2(0u, 0u);
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint32_t* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
 }  // namespace
 
 // ---- launchers ---------------------------------------------------------------------
+hipError_t launch_rmsnorm_f16(const float* x, const float* w, _Float16* yh, int rows, int dim,
+                              int ld, float eps, hipStream_t stream) {
+  const bool ok = dim % 4 == 0 && ld % 4 == 0 && ld >= dim && ((uintptr_t)x & 15) == 0 &&
+                  ((uintptr_t)w & 15) == 0 && ((uintptr_t)yh & 15) == 0;
+  const int per = (dim / 4 + kNormThreads - 1) / kNormThreads;
+  if (!ok || per > 16) return hipErrorInvalidValue;
+  const dim3 grid(rows), block(kNormThreads);
+  if (per <= 1) hipLaunchKernelGGL(rmsnorm_f16_kernel<1>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
+  else if (per <= 2) hipLaunchKernelGGL(rmsnorm_f16_kernel<2>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
+  else if (per <= 4) hipLaunchKernelGGL(rmsnorm_f16_kernel<4>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
+  else if (per <= 8) hipLaunchKernelGGL(rmsnorm_f16_kernel<8>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
+  else hipLaunchKernelGGL(rmsnorm_f16_kernel<16>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {
+  const size_t n = bytes / 4;
+  if (n == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+  fill_zero_kernel<<<blocks, 256, 0, stream>>>((uint32_t*)p, n);
+  return hipGetLastError();
+}
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim,
                           float eps, hipStream_t stream) {
   const bool vec = dim % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&

@@ -429,6 +429,13 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
     }
     return;
   }
+  // output (mrow, col) of y [m][ny]: + residual, fp32 or fp16 store
+  auto put = [&](int mrow, int col, float o) {
+    const size_t idx = (size_t)mrow * a.ny + col;
+    if (a.epi.residual != nullptr) o += a.epi.residual[idx];
+    if (a.epi.yh != nullptr) a.epi.yh[(size_t)mrow * a.epi.yh_ld + col] = (_Float16)o;
+    else a.y[idx] = o;
+  };
   // one code path per (bias, SwiGLU) choice: no per-element branches; the
   // bias depends on the column only, so a lane loads it once per block
   auto store = [&](auto bias_c, auto glu_c) {
@@ -446,10 +453,9 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
           if (GL) {
             // the up row of column ncol (ncol % 16 < 8) is in lane ^ 8
             const float u = __shfl_xor(v, 8);
-            if ((fr & 8) == 0 && ncol < a.n && mrow < a.m)
-              a.y[(size_t)mrow * a.ny + glu_col(ncol)] = silu_f(v) * u;
+            if ((fr & 8) == 0 && ncol < a.n && mrow < a.m) put(mrow, glu_col(ncol), silu_f(v) * u);
           } else if (ncol < a.n && mrow < a.m) {
-            a.y[(size_t)mrow * a.n + ncol] = v;
+            put(mrow, ncol, v);
           }
         }
       }
@@ -508,7 +514,15 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, fl
 #pragma unroll
     for (int e = 0; e < V; ++e) out[e] = add_bias(epi, s[e], c + e);
   }
-  if (VEC) {
+  if (epi.residual != nullptr) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) out[e] += epi.residual[o + e];
+  }
+  if (epi.yh != nullptr) {
+    _Float16* yr = epi.yh + (size_t)r * epi.yh_ld + c;
+#pragma unroll
+    for (int e = 0; e < V; ++e) yr[e] = (_Float16)out[e];
+  } else if (VEC) {
     *(float4*)(y + o) = make_float4(out[0], out[V > 1 ? 1 : 0], out[V > 2 ? 2 : 0], out[V > 3 ? 3 : 0]);
   } else {
     y[o] = out[0];
@@ -645,6 +659,46 @@ hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,
   x_to_f16_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(x, xh, m,
                                                                         k, kp);
   return hipGetLastError();
+}
+
+size_t gemm_partial_bytes(int m, int n, int k) {
+  const int sp = gemm_splits(m, n, k);
+  return sp > 1 ? (size_t)sp * m * n * 4 : 0;
+}
+
+hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, float* y, int m,
+                           void* ws, size_t ws_bytes, hipStream_t stream,
+                           const Epilogue& epi) {
+  const Geometry geo = geometry(w.n, w.k);
+  GemmArgs a;
+  a.qs = (const uint8_t*)w.base + w.qs_off;
+  a.d = (const uint8_t*)w.base + w.d_off;
+  a.mn = w.type == MLQ_Q4_1 ? (const uint8_t*)w.base + w.m_off : nullptr;
+  a.x = nullptr;
+  a.xh = xh;
+  a.y = y;
+  a.m = m;
+  a.n = w.n;
+  a.k = w.k;
+  a.g = geo.g;
+  a.nt = geo.nt;
+  a.kp = f16_row_stride(w.k);
+  a.mtiles = (m + kBM - 1) / kBM;
+  a.ntiles = (geo.nt + kTiles - 1) / kTiles;
+  a.splits = 1;
+  a.part = nullptr;
+  a.epi = epi;
+  a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
+  const int sp = gemm_splits(m, w.n, w.k);
+  if (sp > 1 && ws != nullptr && ws_bytes >= gemm_partial_bytes(m, w.n, w.k)) {
+    a.splits = sp;
+    a.part = (float*)ws;
+  }
+  switch (w.type) {
+    case MLQ_Q8_0: return launch_typed<MLQ_Q8_0>(a, kXF16, stream);
+    case MLQ_Q4_0: return launch_typed<MLQ_Q4_0>(a, kXF16, stream);
+    default: return launch_typed<MLQ_Q4_1>(a, kXF16, stream);
+  }
 }
 
 hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,

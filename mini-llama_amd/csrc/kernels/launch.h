@@ -27,6 +27,15 @@ struct Epilogue {
   // (src/ops.cc:43-72) without a separate pass over x.
   const float* norm = nullptr;  // [k] or nullptr
   float norm_eps = 0.0f;
+  // Prefill GEMM and its split-K reduce only (launch_gemm_ws /
+  // launch_gemm_f16): residual [m][ny] added to the output after the
+  // activation (may alias y: each element is read, then written, by one
+  // thread), and with yh non-null the output is stored as fp16 (round to
+  // nearest even, the rounding of launch_x_to_f16) at yh[r * yh_ld + c]
+  // instead of y.
+  const float* residual = nullptr;
+  _Float16* yh = nullptr;
+  int yh_ld = 0;
 };
 
 // capi.cpp: MLQ status of a HIP result, recorded for mlq_last_hip_error.
@@ -64,6 +73,14 @@ hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
                           void* ws, size_t ws_bytes, hipStream_t stream,
                           const Epilogue& epi = Epilogue());
 size_t f16_copy_bytes(int m, int k);
+// The GEMM from an fp16 copy of x already in place (xh [m][f16_row_stride(k)],
+// zero past k, e.g. written by launch_rmsnorm_f16 or a yh epilogue); `ws`
+// (gemm_partial_bytes(m, n, k), may be null when that is 0) takes the
+// split-K partial slices.
+hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, float* y, int m,
+                           void* ws, size_t ws_bytes, hipStream_t stream,
+                           const Epilogue& epi = Epilogue());
+size_t gemm_partial_bytes(int m, int n, int k);
 int gemm_splits(int m, int n, int k);
 size_t gemm_workspace_bytes(int m, int n, int k);
 // Split-K override (0 = planner); validated by the caller.
@@ -102,6 +119,14 @@ hipError_t launch_linear_f32(const float* w, int n, int k, const float* x, float
 // decode_ops.hip: the decode-step operators.
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, int dim,
                           float eps, hipStream_t stream);
+// RMSNorm rows written as fp16 (round to nearest even) into yh [rows][ld],
+// zero for dim <= c < ld: the GEMM's fp16 copy of its input in one pass.
+// Needs dim % 4 == 0, ld % 4 == 0 and 16-byte aligned x, w, yh rows.
+hipError_t launch_rmsnorm_f16(const float* x, const float* w, _Float16* yh, int rows, int dim,
+                              int ld, float eps, hipStream_t stream);
+// bytes (a multiple of 4) of zeros at p (4-byte aligned): a kernel, so it
+// may be captured in a graph.
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 enum { kEltAdd = 0, kEltMul = 1, kEltSilu = 2, kEltSwiGLU = 3 };
 hipError_t launch_eltwise(int op, const float* a, const float* b, float* y, int64_t n,
                           hipStream_t stream);

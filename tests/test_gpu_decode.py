@@ -554,6 +554,10 @@ PREFILL_CASES = [
     ("f32", {"cfg": {"dim": 128, "n_heads": 4, "n_kv_heads": 2}, "bias": True}, True, 0, 5),
     ("q4_0", {"cfg": {"dim": 128, "n_heads": 4, "n_kv_heads": 1, "hidden_dim": 100}}, True, 2, 1),
     ("q4_0", {"cfg": {"dim": 512, "n_heads": 2, "n_kv_heads": 1, "rope_type": 1}}, True, 0, 9),
+    # prefill GEMM rows with a hidden size off the 128-column grid (the
+    # fp16 SwiGLU output's padding) and biases
+    ("q8_0", {"cfg": {"dim": 256, "n_heads": 4, "n_kv_heads": 2, "hidden_dim": 200},
+              "bias": True}, True, 5, 100),
 ]
 
 
