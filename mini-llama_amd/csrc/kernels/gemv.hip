@@ -30,8 +30,14 @@
 //    the mantissa of 1024 (or 64), one packed fp16 subtract removes the bias.
 //  - MFMA row 2r is the fp16 hi part, row 2r+1 the lo part of activation row
 //    r (x = hi + lo to ~2^-22): up to 8 rows in one MFMA. Per block:
-//    acc += d * (D[hi] + D[lo]) in fp32 (+ m * sum(x) for q4_1). Products
-//    are exact in fp32, so the result is fp32-class accurate.
+//    acc += d * (D[hi] + D[lo]) in fp32. Products are exact in fp32, so the
+//    result is fp32-class accurate.
+//  - q4_1's min term sum_b m_b * sum(x over block b) is one more MFMA per
+//    group: A = the group's four block sums (staged in LDS as fp16 hi/lo
+//    rows, like x), B = the four fp16 mins of the lane's row (exact), K
+//    positions 4..31 zero. Done on the VALU (a float4 of block sums, four
+//    converts and FMAs per group) it held ~60 more registers at depth 6,
+//    which capped how many groups a wave keeps in flight.
 //  - K slices combine through LDS in slice order (deterministic).
 // Activations must be finite and |x| < 65504 (the fp16 range of the hi part).
 #include <hip/hip_runtime.h>
@@ -204,7 +210,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
 
   unsigned char* wl = smem + (size_t)wave * a.wave_lds;
   _Float16* xs = (_Float16*)wl;
-  float* xsum = (float*)(wl + (size_t)2 * M * a.xstride * 2);
+  // q4_1 block sums, per group the MFMA A operand: 16 rows (hi/lo of each
+  // activation row) x 4 halves (the group's blocks)
+  _Float16* xsa = (_Float16*)(wl + (size_t)2 * M * a.xstride * 2);
   float* part = (float*)(smem + (size_t)a.split * a.wave_lds);
 
   // ---- per-wave buffer ranges --------------------------------------------
@@ -267,7 +275,15 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   }
 
   // ---- stage hi/lo activations (+ q4_1 block sums) -----------------------
-  const int nblk = npad * kGroupBlocks;
+  // block sum of row r, block blk (of the slice) -> hi/lo halves at rows
+  // 2r, 2r+1 of group blk/4's A operand
+  auto stage_sum = [&](int r, int blk, float sx) {
+    const _Float16 hi = (_Float16)sx;
+    const _Float16 lo = (_Float16)(sx - (float)hi);
+    _Float16* g = xsa + (size_t)(blk >> 2) * kTileRows * kGroupBlocks + (blk & 3);
+    g[(2 * r) * kGroupBlocks] = hi;
+    g[(2 * r + 1) * kGroupBlocks] = lo;
+  };
 #pragma unroll
   for (int i = 0; i < XR; ++i) {
     const int r = MR == 1 ? 0 : i;
@@ -279,7 +295,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, v);
       if (QT == MLQ_Q4_1) {
         sx = block_sum8(sx);
-        if (c < c4 && (c & 7) == 0) xsum[r * nblk + (c >> 3)] = sx;
+        if (c < c4 && (c & 7) == 0) stage_sum(r, c >> 3, sx);
       }
     }
   }
@@ -297,7 +313,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
         if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, v);
         if (QT == MLQ_Q4_1) {
           sx = block_sum8(sx);
-          if (c < c4 && (c & 7) == 0) xsum[r * nblk + (c >> 3)] = sx;
+          if (c < c4 && (c & 7) == 0) stage_sum(r, c >> 3, sx);
         }
       }
     }
@@ -310,6 +326,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // Rows past 2m read row 0 again: their D rows are never used, and an
   // unmasked read costs no VALU work.
   const _Float16* arow = xs + (size_t)(n < 2 * M ? n : 0) * a.xstride + 8 * kq;
+  const _Float16* asum = xsa + (size_t)(n < 2 * M ? n : 0) * kGroupBlocks;
   const int r0 = 2 * kq, r1 = 2 * kq + 1;  // activation rows of this lane's D
   float acc0 = 0.0f, acc1 = 0.0f;
 
@@ -339,25 +356,27 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       D[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
           __builtin_bit_cast(h8_t, av), bfrag[b], zero, 0, 0, 0);
     }
-    float4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+    // q4_1: sum_b m_b * S_b on the MFMA (A row n: the hi/lo block sums of
+    // activation row n/2 at K 0..3; B: the row's four mins at K 0..3; the
+    // lanes of quarters 1..3 hold K 8..31, all zero)
+    f4_t Dm = zero;
     if (QT == MLQ_Q4_1) {
-      if (r0 < M) s0 = *(const float4*)(xsum + r0 * nblk + j * kGroupBlocks);
-      if (MR > 1 && r1 < M) s1 = *(const float4*)(xsum + r1 * nblk + j * kGroupBlocks);
+      const uint2 sv = kq == 0 ? *(const uint2*)(asum + (size_t)j * kTileRows * kGroupBlocks)
+                               : make_uint2(0u, 0u);
+      const uint4 av = make_uint4(sv.x, sv.y, 0u, 0u);
+      const uint4 bv = kq == 0 ? make_uint4(mm.x, mm.y, 0u, 0u) : make_uint4(0u, 0u, 0u, 0u);
+      Dm = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, av),
+                                                  __builtin_bit_cast(h8_t, bv), zero, 0, 0, 0);
     }
 #pragma unroll
     for (int b = 0; b < kGroupBlocks; ++b) {
       const float df = (float)half_at(dd, b);
       acc0 = fmaf(df, D[b][0] + D[b][1], acc0);
       if (MR > 1) acc1 = fmaf(df, D[b][2] + D[b][3], acc1);
-      if (QT == MLQ_Q4_1) {
-        const float mf = (float)half_at(mm, b);
-        const float e0 = b == 0 ? s0.x : b == 1 ? s0.y : b == 2 ? s0.z : s0.w;
-        acc0 = fmaf(mf, e0, acc0);
-        if (MR > 1) {
-          const float e1 = b == 0 ? s1.x : b == 1 ? s1.y : b == 2 ? s1.z : s1.w;
-          acc1 = fmaf(mf, e1, acc1);
-        }
-      }
+    }
+    if (QT == MLQ_Q4_1) {
+      acc0 += Dm[0] + Dm[1];
+      if (MR > 1) acc1 += Dm[2] + Dm[3];
     }
   };
 
@@ -470,13 +489,14 @@ struct Plan {
 
 // Groups in flight per wave without spilling (VGPR budget of a 1024-thread
 // workgroup): every group of the slice when gw <= max_depth, else a ring.
-// q4_1 carries mins and block sums per group, so its budgets are smaller;
-// one activation row leaves room for ten (long-K shapes with few tiles,
-// e.g. the 3584 x 18944 down-projection, keep more bytes in flight).
+// q4_1 carries mins and block sums per group, so its budgets are smaller
+// (seven groups for one row, a ring of at most four); one activation row
+// leaves room for ten (long-K shapes with few tiles, e.g. the 3584 x 18944
+// down-projection, keep more bytes in flight).
 constexpr int kMaxDepth = 8;
 constexpr int kMaxDepthOneRow = 10;
 int max_depth(int type, int m) {
-  if (type == MLQ_Q4_1) return m == 1 ? 6 : 3;
+  if (type == MLQ_Q4_1) return m == 1 ? 7 : 3;
   return m == 1 ? kMaxDepthOneRow : kMaxDepth;
 }
 // Ring depths that compile without spills, per type and row class.
@@ -509,7 +529,7 @@ size_t wave_lds_bytes(int type, int m, int gw) {
   const int pg = padded_groups(type, m, gw);
   const size_t xstride = (size_t)pg * kGroupK + kRowPadHalves;
   size_t b = (size_t)2 * m * xstride * 2;
-  if (type == MLQ_Q4_1) b += (size_t)m * pg * kGroupBlocks * 4;
+  if (type == MLQ_Q4_1) b += (size_t)pg * kTileRows * kGroupBlocks * 2;  // block sums
   return (b + 15) / 16 * 16;
 }
 
@@ -613,15 +633,15 @@ hipError_t launch_depth(const GemvArgs& a, const Plan& p, hipStream_t stream) {
     case 4: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 4, false>(a, p.lds, stream);
     case 5: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 5, false>(a, p.lds, stream);
     case 6: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 6, false>(a, p.lds, stream);
-    case 7: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 7, false>(a, p.lds, stream);
-    case 8: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 8, false>(a, p.lds, stream);
+    case 7: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 7, false>(a, p.lds, stream);
+    case 8: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 7) : 8, false>(a, p.lds, stream);
     default:
       // 9 and 10: one activation row, q8_0 / q4_0 only
       if constexpr (QT != MLQ_Q4_1 && MR == 1) {
         if (p.depth == 9) return launch_typed<QT, MR, 9, false>(a, p.lds, stream);
         return launch_typed<QT, MR, 10, false>(a, p.lds, stream);
       }
-      return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 6) : 8, false>(a, p.lds, stream);
+      return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 7) : 8, false>(a, p.lds, stream);
   }
 }
 
@@ -641,7 +661,7 @@ bool gemv_norm_supported(const mlq_weight& w) {
   if (p.lds > lds_limit()) return false;
   // the variant launch_depth would pick for this plan
   int depth = p.depth;
-  if (!p.ring && w.type == MLQ_Q4_1) depth = std::min(depth, 6);
+  if (!p.ring && w.type == MLQ_Q4_1) depth = std::min(depth, 7);
   return norm_variant(w.type, depth, p.ring);
 }
 
