@@ -541,15 +541,16 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
   // GEMMs' fp16 inputs directly (RMSNorm rows, the SwiGLU epilogue) and the
   // o / down projections add the residual in their epilogue, which removes
   // four fp16 copy passes and two residual passes per layer with the same
-  // roundings and additions.
+  // roundings and additions (GemmOut).
   auto gemm_rows = [&](const mlq_weight& w) { return n > kSkinnyMaxRows && w.type != MLQ_F32; };
   auto f16_norm_ok = [&](const float* norm) {
     return dim % 4 == 0 && ((uintptr_t)norm & 15) == 0 && dim <= 16 * 4 * 256;
   };
   // (xh rows are f16_row_stride(w.k) halves: w.k is dim or hidden, checked
   // by plan())
-  auto gemm_f16 = [&](const mlq_weight& w, const _Float16* xh, float* y, const Epilogue& e) {
-    return hip(launch_gemm_f16(w, xh, y, n, b.lin, b.lin_bytes, s, e));
+  auto gemm_f16 = [&](const mlq_weight& w, const _Float16* xh, float* y, const Epilogue& e,
+                      const GemmOut& o) {
+    return hip(launch_gemm_f16(w, xh, y, n, b.lin, b.lin_bytes, s, e, o));
   };
   const int ldx = f16_row_stride(dim), ldh = f16_row_stride(hid);
   if (n > kSkinnyMaxRows && ldh > hid) {
@@ -571,7 +572,7 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
       if (!qkv_f16) return linear(w, b.h, y, n, bias, MLQ_EPI_NONE);
       Epilogue e;
       e.bias = bias;
-      return gemm_f16(w, b.xh, y, e);
+      return gemm_f16(w, b.xh, y, e, GemmOut());
     };
     if (qkv_f16)
       rc = hip(launch_rmsnorm_f16(b.x, l.attn_norm, b.xh, n, dim, ldx, m->rms_norm_eps, s));
@@ -650,9 +651,10 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
     }
     // x2 = x + wo . attn (the GEMM adds the residual row by row)
     if (gemm_rows(l.wo)) {
-      Epilogue e;
-      e.residual = b.x;
-      if ((rc = hip(launch_gemm_ws(l.wo, b.attn, b.x2, n, b.lin, b.lin_bytes, s, e))) != MLQ_OK)
+      GemmOut o;
+      o.residual = b.x;
+      if ((rc = hip(launch_gemm_ws(l.wo, b.attn, b.x2, n, b.lin, b.lin_bytes, s, Epilogue(),
+                                   o))) != MLQ_OK)
         return rc;
     } else {
       if ((rc = linear(l.wo, b.attn, b.x2, n, nullptr, MLQ_EPI_NONE)) != MLQ_OK) return rc;
@@ -669,12 +671,13 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
         return rc;
       Epilogue eg;
       eg.act = kEpiSwiGLU;
-      eg.yh = b.gh;
-      eg.yh_ld = ldh;
-      if ((rc = gemm_f16(l.w_gate, b.xh, nullptr, eg)) != MLQ_OK) return rc;
-      Epilogue ed;
-      ed.residual = b.x2;
-      if ((rc = gemm_f16(l.w_down, b.gh, b.x, ed)) != MLQ_OK) return rc;
+      GemmOut og;
+      og.yh = b.gh;
+      og.yh_ld = ldh;
+      if ((rc = gemm_f16(l.w_gate, b.xh, nullptr, eg, og)) != MLQ_OK) return rc;
+      GemmOut od;
+      od.residual = b.x2;
+      if ((rc = gemm_f16(l.w_down, b.gh, b.x, Epilogue(), od)) != MLQ_OK) return rc;
       continue;
     }
     if ((rc = hip(launch_rmsnorm(b.x2, l.ffn_norm, b.h, n, dim, m->rms_norm_eps, s))) != MLQ_OK)

@@ -66,6 +66,7 @@ struct GemmArgs {
   int mtiles, ntiles;  // output tiles
   int splits;          // K ranges per output tile (workgroups per tile)
   Epilogue epi;        // applied here when splits == 1, else by the reduce
+  GemmOut out;         // residual / fp16 output (EXT kernels and the reduce)
   int ny;              // output columns: n, or n/2 under kEpiSwiGLU
 };
 
@@ -254,7 +255,10 @@ struct Slot { static constexpr int v = N; };
 // stage s+2 requested in k step 0 of stage s, stored in its last), which
 // wins only when the grid has more workgroups than CUs (3-8 %; 2-8 % slower
 // on smaller grids), so the launcher picks it by grid size.
-template <int QT, int XM, int OCC = 1, int XS = 2>
+// EXT: the output epilogue also applies GemmOut.residual / GemmOut.yh
+// (a separate instantiation: their per-element branches grow the store code
+// of every kernel by half, which measured 3-6 % slower main loops).
+template <int QT, int XM, int OCC = 1, int XS = 2, bool EXT = false>
 __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
   constexpr int kXS = XS;  // activation register slots (1 or 2)
   __shared__ __align__(16) _Float16 as_buf[3][kBM * kStride];
@@ -432,9 +436,13 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
   // output (mrow, col) of y [m][ny]: + residual, fp32 or fp16 store
   auto put = [&](int mrow, int col, float o) {
     const size_t idx = (size_t)mrow * a.ny + col;
-    if (a.epi.residual != nullptr) o += a.epi.residual[idx];
-    if (a.epi.yh != nullptr) a.epi.yh[(size_t)mrow * a.epi.yh_ld + col] = (_Float16)o;
-    else a.y[idx] = o;
+    if constexpr (EXT) {
+      if (a.out.residual != nullptr) o += a.out.residual[idx];
+      if (a.out.yh != nullptr) a.out.yh[(size_t)mrow * a.out.yh_ld + col] = (_Float16)o;
+      else a.y[idx] = o;
+    } else {
+      a.y[idx] = o;
+    }
   };
   // one code path per (bias, SwiGLU) choice: no per-element branches; the
   // bias depends on the column only, so a lane loads it once per block
@@ -477,7 +485,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
 template <bool VEC>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, float* y,
                                                            int m, int n, int splits,
-                                                           Epilogue epi, int ny) {
+                                                           Epilogue epi, int ny, GemmOut go) {
   constexpr int V = VEC ? 4 : 1;
   const size_t o = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
   if (o >= (size_t)m * ny) return;
@@ -514,12 +522,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, fl
 #pragma unroll
     for (int e = 0; e < V; ++e) out[e] = add_bias(epi, s[e], c + e);
   }
-  if (epi.residual != nullptr) {
+  if (go.residual != nullptr) {
 #pragma unroll
-    for (int e = 0; e < V; ++e) out[e] += epi.residual[o + e];
+    for (int e = 0; e < V; ++e) out[e] += go.residual[o + e];
   }
-  if (epi.yh != nullptr) {
-    _Float16* yr = epi.yh + (size_t)r * epi.yh_ld + c;
+  if (go.yh != nullptr) {
+    _Float16* yr = go.yh + (size_t)r * go.yh_ld + c;
 #pragma unroll
     for (int e = 0; e < V; ++e) yr[e] = (_Float16)out[e];
   } else if (VEC) {
@@ -557,24 +565,34 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const float* x,
   *(uint4*)(xh + (size_t)r * kp + c0) = o;
 }
 
+template <int QT, bool EXT>
+void launch_f16(const GemmArgs& a, unsigned grid, hipStream_t stream) {
+  if constexpr (QT == MLQ_Q4_0)
+    gemm_kernel<QT, kXF16, 2, 2, EXT><<<grid, kThreads, 0, stream>>>(a);
+  else if ((int)grid > device_cus())  // a second workgroup per CU to run
+    gemm_kernel<QT, kXF16, 2, 1, EXT><<<grid, kThreads, 0, stream>>>(a);
+  else
+    gemm_kernel<QT, kXF16, 1, 2, EXT><<<grid, kThreads, 0, stream>>>(a);
+}
+
 template <int QT>
 hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
   const unsigned grid = (unsigned)(a.mtiles * a.ntiles * a.splits);
+  // residual / fp16 output in the GEMM's own store (split K: the reduce
+  // applies them); the prefill paths that set them read the fp16 copy
+  const bool ext = a.splits == 1 && (a.out.residual != nullptr || a.out.yh != nullptr);
+  if (ext && xm != kXF16) return hipErrorInvalidValue;
   switch (xm) {
     case kXF32Vec: gemm_kernel<QT, kXF32Vec><<<grid, kThreads, 0, stream>>>(a); break;
     case kXF32Scalar: gemm_kernel<QT, kXF32Scalar><<<grid, kThreads, 0, stream>>>(a); break;
     default:
-      if constexpr (QT == MLQ_Q4_0)
-        gemm_kernel<QT, kXF16, 2><<<grid, kThreads, 0, stream>>>(a);
-      else if ((int)grid > device_cus())  // a second workgroup per CU to run
-        gemm_kernel<QT, kXF16, 2, 1><<<grid, kThreads, 0, stream>>>(a);
-      else
-        gemm_kernel<QT, kXF16><<<grid, kThreads, 0, stream>>>(a);
+      if (ext) launch_f16<QT, true>(a, grid, stream);
+      else launch_f16<QT, false>(a, grid, stream);
       break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
-  return launch_split_reduce(a.part, a.y, a.m, a.n, a.splits, a.epi, stream);
+  return launch_split_reduce(a.part, a.y, a.m, a.n, a.splits, a.epi, stream, a.out);
 }
 
 int g_split_override = 0;  // mlq_set_gemm_split; 0 = planner
@@ -597,16 +615,16 @@ int device_cus() {
 }
 
 hipError_t launch_split_reduce(const float* part, float* y, int m, int n, int splits,
-                               const Epilogue& epi, hipStream_t stream) {
+                               const Epilogue& epi, hipStream_t stream, const GemmOut& out) {
   const int ny = epi.act == kEpiSwiGLU ? n / 2 : n;
   const size_t outs = (size_t)m * ny;
   if (n % 4 == 0) {
     const size_t threads = outs / 4;
     split_reduce_kernel<true><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
-        part, y, m, n, splits, epi, ny);
+        part, y, m, n, splits, epi, ny, out);
   } else {
     split_reduce_kernel<false><<<(unsigned)((outs + 255) / 256), 256, 0, stream>>>(
-        part, y, m, n, splits, epi, ny);
+        part, y, m, n, splits, epi, ny, out);
   }
   return hipGetLastError();
 }
@@ -668,7 +686,7 @@ size_t gemm_partial_bytes(int m, int n, int k) {
 
 hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, float* y, int m,
                            void* ws, size_t ws_bytes, hipStream_t stream,
-                           const Epilogue& epi) {
+                           const Epilogue& epi, const GemmOut& out) {
   const Geometry geo = geometry(w.n, w.k);
   GemmArgs a;
   a.qs = (const uint8_t*)w.base + w.qs_off;
@@ -688,6 +706,7 @@ hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, float* y, in
   a.splits = 1;
   a.part = nullptr;
   a.epi = epi;
+  a.out = out;
   a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
   const int sp = gemm_splits(m, w.n, w.k);
   if (sp > 1 && ws != nullptr && ws_bytes >= gemm_partial_bytes(m, w.n, w.k)) {
@@ -708,7 +727,7 @@ hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
 
 hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
                           void* ws, size_t ws_bytes, hipStream_t stream,
-                          const Epilogue& epi) {
+                          const Epilogue& epi, const GemmOut& out) {
   const Geometry geo = geometry(w.n, w.k);
   GemmArgs a;
   a.qs = (const uint8_t*)w.base + w.qs_off;
@@ -728,6 +747,7 @@ hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
   a.splits = 1;
   a.part = nullptr;
   a.epi = epi;
+  a.out = out;
   a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
   // every activation row offset of a workgroup must fit a 32-bit buffer
   // offset

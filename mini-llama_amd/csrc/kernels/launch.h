@@ -27,12 +27,17 @@ struct Epilogue {
   // (src/ops.cc:43-72) without a separate pass over x.
   const float* norm = nullptr;  // [k] or nullptr
   float norm_eps = 0.0f;
-  // Prefill GEMM and its split-K reduce only (launch_gemm_ws /
-  // launch_gemm_f16): residual [m][ny] added to the output after the
-  // activation (may alias y: each element is read, then written, by one
-  // thread), and with yh non-null the output is stored as fp16 (round to
-  // nearest even, the rounding of launch_x_to_f16) at yh[r * yh_ld + c]
-  // instead of y.
+};
+
+// Output options of the prefill GEMM reading the fp16 copy of x and of its
+// split-K reduce (launch_gemm_f16, launch_gemm_ws with a workspace that
+// holds the copy; else hipErrorInvalidValue): residual [m][ny] added to the
+// output after the activation (may alias y: each element is read, then
+// written, by one thread), and with yh non-null the output is stored as
+// fp16 (round to nearest even, the rounding of launch_x_to_f16) at
+// yh[r * yh_ld + c] instead of y. Kept out of Epilogue so that the other
+// kernels' arguments do not grow.
+struct GemmOut {
   const float* residual = nullptr;
   _Float16* yh = nullptr;
   int yh_ld = 0;
@@ -71,7 +76,7 @@ hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream);
 hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
                           void* ws, size_t ws_bytes, hipStream_t stream,
-                          const Epilogue& epi = Epilogue());
+                          const Epilogue& epi = Epilogue(), const GemmOut& out = GemmOut());
 size_t f16_copy_bytes(int m, int k);
 // The GEMM from an fp16 copy of x already in place (xh [m][f16_row_stride(k)],
 // zero past k, e.g. written by launch_rmsnorm_f16 or a yh epilogue); `ws`
@@ -79,7 +84,7 @@ size_t f16_copy_bytes(int m, int k);
 // split-K partial slices.
 hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, float* y, int m,
                            void* ws, size_t ws_bytes, hipStream_t stream,
-                           const Epilogue& epi = Epilogue());
+                           const Epilogue& epi = Epilogue(), const GemmOut& out = GemmOut());
 size_t gemm_partial_bytes(int m, int n, int k);
 int gemm_splits(int m, int n, int k);
 size_t gemm_workspace_bytes(int m, int n, int k);
@@ -95,7 +100,8 @@ int device_cus();
 // y = epilogue(sum over s of part[s] in order), part [splits][m][n] fp32
 // (split-K partial slices of the prefill and skinny GEMMs).
 hipError_t launch_split_reduce(const float* part, float* y, int m, int n, int splits,
-                               const Epilogue& epi, hipStream_t stream);
+                               const Epilogue& epi, hipStream_t stream,
+                               const GemmOut& out = GemmOut());
 
 // skinny.hip: 9..64 rows of x. launch_skinny_ws makes the fragment-ordered
 // fp16 copy of x in ws, then runs the skinny GEMM (K split over
