@@ -222,7 +222,10 @@ def test_attention_reference_cases(pkg, oracle, cuda):
     (16, 1, 256, 600, 599), (16, 16, 80, 100, 99), (4, 2, 8, 128, 127), (6, 3, 4, 40, 33),
     (32, 2, 100, 300, 150), (64, 4, 64, 200, 129),
     # seven query heads per kv head (padded to eight in the kernels)
-    (14, 2, 64, 300, 200), (7, 1, 256, 200, 150), (21, 3, 96, 100, 60)])
+    (14, 2, 64, 300, 200), (7, 1, 256, 200, 150), (21, 3, 96, 100, 60),
+    # more than 128 chunk partials per head (the combine's register-held
+    # maxima and sums overflow into reads from memory)
+    (8, 2, 128, 9100, 9000), (6, 3, 96, 4600, 4500)])
 def test_attention_matches_oracle(pkg, oracle, cuda, n_heads, n_kv, hd, max_seq, pos):
     rng = np.random.default_rng(pos * 7 + hd)
     keys = rng.standard_normal((2, max_seq, n_kv, hd)).astype(np.float32)
