@@ -364,29 +364,32 @@ def bench_prefill(dm, torch, n, reps):
             "linear_tflops": flops / (ms * 1e-3) / 1e12, "reps": reps}
 
 
-def cpu_baseline(qtype, n, k, budget_s=10.0):
-    """The reference CPU path (oracle restatement of linearQ40 with the
-    reference thread partition), timed on this host's cores."""
+def cpu_baseline(qtype, n, k, budget_s=10.0, flavor="scalar"):
+    """The reference CPU path (oracle restatement of linearQ40 / linearQ80
+    with the reference thread partition), timed on this host's cores; flavor
+    "avx2" is the build with the reference's AVX2 q8_0 loop (quant.cc:505-628;
+    q4_0 / q4_1 have no SIMD path there, quant.cc:637-650)."""
     oracle = graft.load_oracle()
     graft.load_package()
     import mini_llama_amd.synth as synth
     threads = max(1, min(16, os.cpu_count() or 1))
     blocks = synth.make_blocks(qtype, n, k, 1)
     x = synth.make_x(1, k, 2)[0]
-    oracle.linear(x, blocks, (n, k), qtype, threads=threads)  # warm
+    oracle.linear(x, blocks, (n, k), qtype, threads=threads, flavor=flavor)  # warm
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.linear(x, blocks, (n, k), qtype, threads=threads)
+        oracle.linear(x, blocks, (n, k), qtype, threads=threads, flavor=flavor)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 1000:
             break
     per = el / reps
+    build = "scalar -O2" if flavor == "scalar" else "-O2 -mavx2 -mfma"
     return {"value": alg_bytes(qtype, 1, n, k) / per / 1e9, "unit": "GB/s",
             "cores": threads, "kind": "port",
             "sample": f"{reps} full {qtype} GEMV calls W[{n},{k}] M=1 "
                       f"({per * 1e3:.2f} ms/call, {threads} threads, "
-                      f"scalar -O2 build of oracle/quant_ref.c)"}
+                      f"{build} build of oracle/quant_ref.c)"}
 
 
 def main():
@@ -499,6 +502,21 @@ def main():
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline("q4_0", 18944, 3584, args.cpu_budget)
         result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 3)
+        # the same CPU path with and without the reference's AVX2 build, on
+        # the headline shape and on configs[0] (q8_0, the type with an AVX2
+        # loop), a few seconds each
+        oracle = graft.load_oracle()
+        variants = []
+        for qt, n, k, tag in (("q4_0", 18944, 3584, "configs[1]"),
+                              ("q8_0", 4096, 4096, "configs[0]")):
+            for flavor in ("scalar", "avx2"):
+                if (qt, flavor) == ("q4_0", "scalar") or not oracle.flavor_available(flavor):
+                    continue
+                v = cpu_baseline(qt, n, k, min(3.0, args.cpu_budget), flavor)
+                variants.append({"config": tag, "build": flavor,
+                                 "value": round(v["value"], 3), "unit": "GB/s",
+                                 "cores": v["cores"], "sample": v["sample"]})
+        result["cpu_baseline_builds"] = variants
     print(json.dumps(result), flush=True)
 
 
