@@ -563,6 +563,10 @@ PREFILL_CASES = [
     # fp16 SwiGLU output's padding) and biases
     ("q8_0", {"cfg": {"dim": 256, "n_heads": 4, "n_kv_heads": 2, "hidden_dim": 200},
               "bias": True}, True, 5, 100),
+    # F32 weights with more than 64 rows (no prefill GEMM: the unfused path)
+    # and q4_1 fused with biases through the prefill GEMM
+    ("f32", {"cfg": {"dim": 128, "n_heads": 4, "n_kv_heads": 2}, "bias": True}, True, 2, 70),
+    ("q4_1", {"cfg": {"dim": 256, "n_heads": 8, "n_kv_heads": 2}, "bias": True}, True, 0, 129),
 ]
 
 
