@@ -157,6 +157,7 @@ struct PrefillBuffers {
   // producers (RMSNorm rows, the gate|up SwiGLU epilogue)
   _Float16* xh;     // [n][f16_row_stride(dim)]
   _Float16* gh;     // [n][f16_row_stride(hidden)]
+  _Float16* ah;     // [n][f16_row_stride(n_heads * head_dim)] (attention output)
   size_t total;
 };
 
@@ -212,6 +213,7 @@ int plan_prefill(const mlq_model* m, int n, char* base, PrefillBuffers* b) {
   const bool gemm_rows = n > kSkinnyMaxRows;
   b->xh = gemm_rows ? (_Float16*)take(rows * f16_row_stride(dim) * 2) : nullptr;
   b->gh = gemm_rows ? (_Float16*)take(rows * f16_row_stride(hid) * 2) : nullptr;
+  b->ah = gemm_rows ? (_Float16*)take(rows * f16_row_stride(qd) * 2) : nullptr;
   b->total = off;
   return MLQ_OK;
 }
@@ -552,11 +554,14 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
                       const GemmOut& o) {
     return hip(launch_gemm_f16(w, xh, y, n, b.lin, b.lin_bytes, s, e, o));
   };
-  const int ldx = f16_row_stride(dim), ldh = f16_row_stride(hid);
+  const int ldx = f16_row_stride(dim), ldh = f16_row_stride(hid), ldq = f16_row_stride(qd);
+  // the SwiGLU epilogue and the attention kernel write their columns only;
+  // the GEMMs reading them need zeros up to the padded row length
   if (n > kSkinnyMaxRows && ldh > hid) {
-    // the SwiGLU epilogue writes hidden columns only; the GEMM reading them
-    // needs zeros up to the padded row length
     if ((rc = hip(launch_fill_zero(b.gh, (size_t)n * ldh * 2, s))) != MLQ_OK) return rc;
+  }
+  if (n > kSkinnyMaxRows && ldq > qd) {
+    if ((rc = hip(launch_fill_zero(b.ah, (size_t)n * ldq * 2, s))) != MLQ_OK) return rc;
   }
   if ((rc = hip(hipMemcpyAsync(b.tokens, tokens, (size_t)n * sizeof(int32_t),
                                hipMemcpyHostToDevice, s))) != MLQ_OK)
@@ -612,6 +617,8 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
     // kernel over blocks of query rows
     const bool mfma_attn = prefill_attention_supported(hd, m->n_heads / m->n_kv_heads) &&
                            ((uintptr_t)c->keys & 15) == 0 && ((uintptr_t)c->values & 15) == 0;
+    // the attention kernel writes the o projection's fp16 input directly
+    const bool attn_f16 = mfma_attn && gemm_rows(l.wo);
     if (mfma_attn) {
       AttnLaunch a;
       a.q = rr.q;
@@ -626,7 +633,8 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
       a.pos = start_pos;
       a.rows = n;
       a.q_stride = rr.q_stride;
-      a.out_stride = qd;
+      a.out_stride = attn_f16 ? ldq : qd;
+      a.out_h = attn_f16 ? b.ah : nullptr;
       if ((rc = hip(launch_attention_prefill(a, s))) != MLQ_OK) return rc;
     }
     for (int r0 = 0; !mfma_attn && r0 < n; r0 += kPrefillAttnRows) {
@@ -650,7 +658,11 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
       if ((rc = hip(launch_attention(a, s))) != MLQ_OK) return rc;
     }
     // x2 = x + wo . attn (the GEMM adds the residual row by row)
-    if (gemm_rows(l.wo)) {
+    if (attn_f16) {
+      GemmOut o;
+      o.residual = b.x;
+      if ((rc = gemm_f16(l.wo, b.ah, b.x2, Epilogue(), o)) != MLQ_OK) return rc;
+    } else if (gemm_rows(l.wo)) {
       GemmOut o;
       o.residual = b.x;
       if ((rc = hip(launch_gemm_ws(l.wo, b.attn, b.x2, n, b.lin, b.lin_bytes, s, Epilogue(),

@@ -347,6 +347,9 @@ struct AttnArgs {
   // q + r * q_stride, writes out + r * out_stride; partials are [rows] x
   // [n_heads] x [chunks]. One row for a decode step.
   int rows, q_stride, out_stride;
+  // prefill kernel only: with out_h non-null the output rows are written as
+  // fp16 (round to nearest even) at out_h + r * out_stride instead of out
+  _Float16* out_h;
   const int32_t* pos_dev;
   int pos;
   float scale;
@@ -905,7 +908,9 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
       lsum += mml[W * 16 + w * 16 + m] * f;
       o += macc[(w * 16 + m) * HD + d] * f;
     }
-    a.out[(size_t)qr * a.out_stride + (size_t)(kvh * G + m % GP) * HD + d] = o / lsum;
+    const size_t at = (size_t)qr * a.out_stride + (size_t)(kvh * G + m % GP) * HD + d;
+    if (a.out_h != nullptr) a.out_h[at] = (_Float16)(o / lsum);
+    else a.out[at] = o / lsum;
   }
 }
 
@@ -1326,6 +1331,7 @@ static void attn_launch_g(const AttnArgs& a, hipStream_t stream) {
 
 hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   AttnArgs a;
+  a.out_h = nullptr;  // (prefill kernel only)
   a.q = r.q;
   a.keys = r.keys;
   a.values = r.values;
@@ -1403,6 +1409,7 @@ hipError_t launch_attention_prefill(const AttnLaunch& r, hipStream_t stream) {
   a.rows = r.rows;
   a.q_stride = r.q_stride;
   a.out_stride = r.out_stride;
+  a.out_h = r.out_h;
   a.scale = sqrtf(1.0f / (float)r.hd);
   if (!prefill_attention_supported(r.hd, a.group) || ((uintptr_t)r.keys & 15) != 0 ||
       ((uintptr_t)r.values & 15) != 0)

@@ -192,6 +192,9 @@ struct AttnLaunch {
   // pos + r, q row r at q + r * q_stride, output row at out + r * out_stride;
   // ws holds attention_workspace_bytes(n_heads, hd, max_len, rows).
   int rows = 1, q_stride = 0, out_stride = 0;
+  // launch_attention_prefill only: fp16 output rows (round to nearest
+  // even) at out_h + r * out_stride instead of out
+  _Float16* out_h = nullptr;
 };
 bool attention_supported(int n_heads, int n_kv, int hd);
 bool attention_fusable(int hd, int group);
