@@ -12,7 +12,9 @@ on the stream they run on.
 Also reported in the same line: the q8_0 prefill GEMM (configs[4], M=512,
 W [11008, 4096]) in TFLOP/s against the dense fp16 MFMA peak, and the
 reference CPU path (the oracle restatement) timed on the host cores.
-`--all` adds every BASELINE configuration and the 196-GEMV decode sweep.
+`configs` holds the other BASELINE configurations (configs[0], [2] and [3]
+at M = 4, 16, 64) in GB/s and fraction of 8 TB/s; `--all` adds the
+196-GEMV decode sweeps and the GGUF upload rate.
 `decode_step` reports whole-model decode: a Qwen2-7B-shaped q4_0
 model stepped token by token through mlq_decode_token, captured with its
 greedy sampling as one HIP graph, in tokens/s and algorithmic GB/s (weights
@@ -398,7 +400,7 @@ def main():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--all", action="store_true",
-                    help="also run every BASELINE config and the decode sweep")
+                    help="also run the decode sweeps and the GGUF upload timing")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--mode", choices=["full", "headline", "copy", "decode"],
@@ -477,17 +479,19 @@ def main():
     except Exception as e:  # reported, never fatal to the headline line
         result["decode_step"] = {"error": f"{type(e).__name__}: {e}"}
     torch.cuda.empty_cache()
+    # every other BASELINE config (GEMV / skinny shapes), a few seconds each
+    extra = {}
+    for name, qt, m, n, k in [("c0", "q8_0", 1, 4096, 4096),
+                              ("c2", "q4_1", 1, 4096, 14336),
+                              ("c3_m4", "q4_0", 4, 4096, 4096),
+                              ("c3_m16", "q4_0", 16, 4096, 4096),
+                              ("c3_m64", "q4_0", 64, 4096, 4096)]:
+        r = bench_case(pkg, torch, qt, m, n, k, args.steps, args.warmup, 100)
+        extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
+                       for kk, v in r.items()}
+        extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+    result["configs"] = extra
     if args.all:
-        extra = {}
-        for name, qt, m, n, k in [("c0", "q8_0", 1, 4096, 4096),
-                                  ("c2", "q4_1", 1, 4096, 14336),
-                                  ("c3_m4", "q4_0", 4, 4096, 4096),
-                                  ("c3_m16", "q4_0", 16, 4096, 4096),
-                                  ("c3_m64", "q4_0", 64, 4096, 4096)]:
-            r = bench_case(pkg, torch, qt, m, n, k, args.steps, args.warmup, 100)
-            extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
-                           for kk, v in r.items()}
-            extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
         for mode, key in (("separate", "sweep"), ("fused", "sweep_fused"),
                           ("epilogue", "sweep_epilogue")):
             sw = bench_sweep(pkg, torch, max(1, args.steps // 100), 1, mode)
