@@ -936,12 +936,18 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   const float* pm = pp.m + (size_t)head * a.chunks;
   const float* pl = pp.l + (size_t)head * a.chunks;
   const float* pa = pp.acc + (size_t)head * a.chunks * a.hd;
-  float mx = -INFINITY;
-  for (int c = lane; c < chunks; c += 64) mx = fmaxf(mx, pm[c]);
-  mx = wave_max(mx);
-  float denom = 0.0f;
-  for (int c = lane; c < chunks; c += 64) denom += pl[c] * expf(pm[c] - mx);
-  denom = wave_sum(denom);
+  // global max and sum in one pass over the partials: each lane keeps a
+  // running (max, sum rescaled to it), then the lanes' pairs are merged
+  float mx = -INFINITY, ls = 0.0f;
+  for (int c = lane; c < chunks; c += 64) {
+    const float m = pm[c], l = pl[c];
+    const float nm = fmaxf(mx, m);
+    ls = (mx == -INFINITY ? 0.0f : ls * expf(mx - nm)) + (m == -INFINITY ? 0.0f : l * expf(m - nm));
+    mx = nm;
+  }
+  const float gmx = wave_max(mx);
+  const float denom = wave_sum(mx == -INFINITY ? 0.0f : ls * expf(mx - gmx));
+  mx = gmx;
   constexpr int kD = kAttnMaxHd / 64;
   float acc[kD];
 #pragma unroll
