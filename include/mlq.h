@@ -46,6 +46,7 @@ enum mlq_status {
   MLQ_ERR_UNSUPPORTED = -5,      /* shape outside what the kernels accept  */
   MLQ_ERR_NO_DEVICE = -6,        /* no usable HIP device                   */
   MLQ_ERR_FORMAT = -7,           /* malformed GGUF file, see mlq_gguf_last_error */
+  MLQ_ERR_SCRATCH_LIMIT = -8,    /* needs more than the fixed no-alloc scratch */
   MLQ_ERR_HIP = -100             /* HIP runtime error, see mlq_last_hip_error */
 };
 
@@ -257,6 +258,23 @@ int mlq_set_gemm_split(int split);
  * finish sums in range order; 0 leaves that choice to the planner. Query
  * mlq_linear_workspace after changing it. MLQ_ERR_INVALID_ARG otherwise. */
 int mlq_set_skinny_plan(int tiles, int splits);
+
+/* mlq_linear_epi that allocates nothing and takes no workspace: no
+ * counterpart in the reference. For callers that cannot call hipMalloc
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). The scratch that mlq_linear_epi keeps in the caller's
+ * workspace (fp16 copy of x, split-K partial slices) comes from a fixed
+ * array of MLQ_NOALLOC_SCRATCH_BYTES in the library's device code, one per
+ * GPU, held until the process ends. Shapes whose mlq_linear_workspace
+ * exceeds that size return MLQ_ERR_SCRATCH_LIMIT (the decode GEMV and F32
+ * weights need none). Same kernels and bit-identical results as
+ * mlq_linear_epi. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams, or host threads) race and must be
+ * ordered by the caller. The device is the stream's (the current device for
+ * the null stream). */
+#define MLQ_NOALLOC_SCRATCH_BYTES (64u << 20)
+int mlq_linear_epi_noalloc(const mlq_weight* w, const float* x, float* y, int m,
+                           const float* bias, int act, mlq_stream_t stream);
 
 /* Add bias[n] to every row of y[m, n] on the device (the reference adds the
  * bias on the host after download, src/cuda_quant.cu:229-235, 327-329). */

@@ -36,6 +36,7 @@ STATUS = {
     0: "ok", -1: "invalid argument", -2: "shape mismatch",
     -3: "block count mismatch", -4: "buffer too small",
     -5: "unsupported shape", -6: "no HIP device", -7: "malformed GGUF file",
+    -8: "shape needs more than the fixed no-alloc scratch",
     -100: "HIP runtime error",
 }
 
@@ -126,6 +127,7 @@ SIGNATURES = {
     "mlq_linear_workspace": ([_WP, _I, ctypes.POINTER(_Z)], _I),
     "mlq_linear_ws": ([_WP, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_linear_epi": ([_WP, _P, _P, _I, _P, _I, _P, _Z, _P], _I),
+    "mlq_linear_epi_noalloc": ([_WP, _P, _P, _I, _P, _I, _P], _I),
     "mlq_interleave_rows": ([_P, _P, _I, _Z, _P], _I),
     "mlq_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(_P)], _I),
     "mlq_gguf_last_error": ([], ctypes.c_char_p),
@@ -483,6 +485,27 @@ def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None,
     _check(lib().mlq_linear_path(ctypes.byref(w.layout), x.data_ptr(),
                                  y.data_ptr(), m, path, _stream(stream)),
            "mlq_linear")
+    return y
+
+
+def linear_noalloc(w: TiledWeight, x, y=None, bias=None, act: int = EPI_NONE,
+                   stream=None):
+    """mlq_linear_epi_noalloc: linear() with the library's fixed per-GPU
+    scratch instead of a workspace (no allocation inside the call)."""
+    import torch
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float32 device tensor")
+    m = 1 if x.dim() == 1 else x.shape[0]
+    if x.shape[-1] != w.k:
+        raise ValueError(f"in_features mismatch: x has {x.shape[-1]}, weight has {w.k}")
+    ny = w.n // 2 if act == EPI_SWIGLU else w.n
+    if y is None:
+        shape = (ny,) if x.dim() == 1 else (m, ny)
+        y = torch.empty(shape, dtype=torch.float32, device=x.device)
+    _check(lib().mlq_linear_epi_noalloc(ctypes.byref(w.layout), x.data_ptr(), y.data_ptr(), m,
+                                        bias.data_ptr() if bias is not None else None,
+                                        act, _stream(stream)),
+           "mlq_linear_epi_noalloc")
     return y
 
 

@@ -86,6 +86,7 @@ const char* mlq_status_string(int status) {
     case MLQ_ERR_UNSUPPORTED: return "unsupported shape";
     case MLQ_ERR_NO_DEVICE: return "no HIP device";
     case MLQ_ERR_FORMAT: return "malformed GGUF file";
+    case MLQ_ERR_SCRATCH_LIMIT: return "shape needs more than the fixed no-alloc scratch";
     case MLQ_ERR_HIP: return "HIP runtime error";
     default: return "unknown status";
   }
