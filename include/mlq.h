@@ -254,8 +254,8 @@ int mlq_set_gemm_split(int split);
 /* Skinny GEMM (9..64 rows) plan override for tuning and tests
  * (process-wide): `tiles` weight tiles of 16 rows per workgroup (1, 2 or 4)
  * and `splits` K ranges per tile group (1..8; ranges beyond the number of
- * 128-k groups are capped), whose fp32 partials the last workgroup to
- * finish sums in range order; 0 leaves that choice to the planner. Query
+ * 128-k groups are capped), whose fp32 partial slices a second kernel sums
+ * in range order; 0 leaves that choice to the planner. Query
  * mlq_linear_workspace after changing it. MLQ_ERR_INVALID_ARG otherwise. */
 int mlq_set_skinny_plan(int tiles, int splits);
 
@@ -309,6 +309,10 @@ int mlq_add(const float* a, const float* b, float* y, int64_t n, mlq_stream_t st
 int mlq_mul(const float* a, const float* b, float* y, int64_t n, mlq_stream_t stream);
 int mlq_silu(const float* x, float* y, int64_t n, mlq_stream_t stream);
 int mlq_swiglu(const float* gate, const float* up, float* y, int64_t n, mlq_stream_t stream);
+/* y[n] = exp(x - max(x)) / sum(exp(x - max(x))) over one vector (softmax,
+ * src/ops.cc:74-109; cudaSoftmax, include/mini_llama/cuda_ops.h:68). x and
+ * y may alias. */
+int mlq_softmax(const float* x, float* y, int64_t n, mlq_stream_t stream);
 /* y[dim] = table[token] of an fp32 [vocab, dim] table
  * (cudaEmbeddingLookupDeviceWeight, cuda_ops.h:71); token outside
  * [0, vocab) is MLQ_ERR_INVALID_ARG. */

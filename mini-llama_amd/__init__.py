@@ -148,6 +148,7 @@ SIGNATURES = {
     "mlq_mul": ([_P, _P, _P, _I64, _P], _I),
     "mlq_silu": ([_P, _P, _I64, _P], _I),
     "mlq_swiglu": ([_P, _P, _P, _I64, _P], _I),
+    "mlq_softmax": ([_P, _P, _I64, _P], _I),
     "mlq_embedding": ([_P, _I, _I, _I, _P, _P], _I),
     "mlq_rope": ([_P, _P, _I, _I, _I, _I, _F, _I, _P], _I),
     "mlq_kv_cache_bytes": ([_I, _I, _I, _I, ctypes.POINTER(_Z)], _I),

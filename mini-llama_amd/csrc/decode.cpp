@@ -251,6 +251,12 @@ int mlq_swiglu(const float* gate, const float* up, float* y, int64_t n, mlq_stre
   return eltwise(kEltSwiGLU, gate, up, y, n, stream);
 }
 
+int mlq_softmax(const float* x, float* y, int64_t n, mlq_stream_t stream) {
+  if (x == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (n <= 0) return MLQ_ERR_SHAPE;
+  return record_hip(launch_softmax(x, y, n, (hipStream_t)stream));
+}
+
 int mlq_embedding(const float* table, int vocab, int dim, int token, float* y,
                   mlq_stream_t stream) {
   if (table == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
@@ -455,6 +461,7 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
       r.neox = m->rope_type == MLQ_ROPE_NEOX;
       r.layer = li;
       r.max_seq = c->max_seq_len;
+      r.pos_limit = m->max_seq_len;
       r.pos_dev = pos_dev;
       r.pos = pos;
       r.theta = m->rope_theta;
@@ -472,6 +479,9 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     a.n_kv = m->n_kv_heads;
     a.hd = hd;
     a.max_len = pos_dev != nullptr ? m->max_seq_len : pos + 1;
+    // the model's limit (the cache may be larger): forwardToken's
+    // pos < max_seq_len rule (src/forward.cc:42) for device positions
+    a.pos_limit = m->max_seq_len;
     a.pos_dev = pos_dev;
     a.pos = pos;
     if (fused_rope) {

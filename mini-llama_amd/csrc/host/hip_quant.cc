@@ -12,22 +12,15 @@
 #include <string>
 #include <vector>
 
+#include "host_common.h"
+#include "mini_llama/hip_matmul.h"
 #include "mlq.h"
 
 namespace mini_llama {
 namespace {
 
 // Status -> exception in the style of checkCudaQuant (src/cuda_quant.cu:20-29).
-void checkStatus(int rc, const char* what) {
-  if (rc == MLQ_OK) return;
-  if (rc == MLQ_ERR_HIP) {
-    throw std::runtime_error(
-        "HIP quant error in " + std::string(what) + ": " +
-        hipGetErrorString(static_cast<hipError_t>(mlq_last_hip_error())));
-  }
-  throw std::runtime_error("HIP quant error in " + std::string(what) + ": " +
-                           mlq_status_string(rc));
-}
+void checkStatus(int rc, const char* what) { checkMlq(rc, "HIP quant error in", what); }
 
 int quantInFeatures(const std::vector<int>& x_shape, const std::string& x_str,
                     const char* caller) {
@@ -103,29 +96,6 @@ void addBiasInPlace(Tensor& y, const Tensor& bias, int rows, int cols) {
       y.data[static_cast<size_t>(row) * cols + col] += bias.data[col];
 }
 
-// Grow-only per-device workspace for repacking raw AoS weights. Work on the
-// null stream is ordered, so reuse across calls is safe; hipFree of an old,
-// smaller buffer waits for the device.
-void* aosWorkspace(int device_id, size_t bytes) {
-  static std::mutex mu;
-  static std::map<int, HipDeviceBuffer> buffers;
-  std::lock_guard<std::mutex> lock(mu);
-  HipDeviceBuffer& buf = buffers[device_id];
-  if (buf.bytes() < bytes) buf.reset(bytes, device_id);
-  return buf.data();
-}
-
-// Grow-only per-device workspace for the prefill GEMM's fp16 copy of x
-// (mlq_linear_ws). Null-stream ordering makes reuse across calls safe.
-void* activationWorkspace(int device_id, size_t bytes) {
-  static std::mutex mu;
-  static std::map<int, HipDeviceBuffer> buffers;
-  std::lock_guard<std::mutex> lock(mu);
-  HipDeviceBuffer& buf = buffers[device_id];
-  if (buf.bytes() < bytes) buf.reset(bytes, device_id);
-  return buf.data();
-}
-
 // Runs y = x W^T for a device weight pointer: a registered tiled buffer goes
 // straight to the kernels, anything else is taken as GGUF AoS blocks.
 void runLinear(int type, const void* w_dev, size_t block_count,
@@ -142,15 +112,16 @@ void runLinear(int type, const void* w_dev, size_t block_count,
     size_t ws_bytes = 0;
     rc = mlq_linear_workspace(&layout, p.rows, &ws_bytes);
     checkStatus(rc, caller);
-    void* ws = ws_bytes ? activationWorkspace(device_id, ws_bytes) : nullptr;
-    rc = mlq_linear_ws(&layout, x, y, p.rows, ws, ws_bytes, nullptr);
+    Workspace ws;
+    if (ws_bytes) ws = deviceWorkspace(kActivationWorkspace, device_id, ws_bytes);
+    rc = mlq_linear_ws(&layout, x, y, p.rows, ws.data, ws_bytes, nullptr);
   } else {
     mlq_weight need;
     rc = mlq_weight_layout(type, p.out_features, p.in_features, &need);
     checkStatus(rc, caller);
-    void* ws = aosWorkspace(device_id, need.bytes);
+    Workspace ws = deviceWorkspace(kAosWorkspace, device_id, need.bytes);
     rc = mlq_linear_aos(type, w_dev, block_count, p.out_features, p.in_features,
-                        x, y, p.rows, ws, need.bytes, nullptr);
+                        x, y, p.rows, ws.data, need.bytes, nullptr);
   }
   checkStatus(rc, "mlq_linear");
 }
@@ -295,12 +266,14 @@ HipTensor hipQ41LinearDeviceInput(const HipTensor& x, const void* q4_1_device,
 HipTensor hipLinearUploaded(const HipTensor& x, const HipUploadedWeight& weight,
                             int device_id) {
   static constexpr const char* kCaller = "hipLinearUploaded";
-  if (weight.type == QuantType::kF32)
-    throw std::runtime_error(std::string(kCaller) +
-                             ": F32 weights are not handled by the HIP quant path");
   if (x.deviceId() != device_id || weight.buffer.device_id() != device_id)
     throw std::runtime_error(std::string(kCaller) +
                              ": tensors on different HIP devices");
+  if (weight.type == QuantType::kF32) {
+    // F32 projections: the fp32 GEMV over the raw rows, as forwardLinearDevice
+    // sends them to cudaLinearDeviceInput (src/forward.cc:206-209)
+    return hipLinearDeviceInput(x, weight.buffer.data(), weight.shape, device_id);
+  }
   validateQuantLinearShape(x.shape(), x.shapeString(), weight.shape,
                            weight.block_count, 32, kCaller);
   hipSetDeviceId(device_id);
@@ -308,9 +281,10 @@ HipTensor hipLinearUploaded(const HipTensor& x, const HipUploadedWeight& weight,
   HipTensor y(outputShape(p), device_id);
   size_t ws_bytes = 0;
   checkStatus(mlq_linear_workspace(&weight.layout, p.rows, &ws_bytes), kCaller);
-  void* ws = ws_bytes ? activationWorkspace(device_id, ws_bytes) : nullptr;
+  Workspace ws;
+  if (ws_bytes) ws = deviceWorkspace(kActivationWorkspace, device_id, ws_bytes);
   checkStatus(mlq_linear_ws(&weight.layout, static_cast<const float*>(x.data()),
-                            static_cast<float*>(y.data()), p.rows, ws, ws_bytes,
+                            static_cast<float*>(y.data()), p.rows, ws.data, ws_bytes,
                             nullptr),
               "mlq_linear_ws");
   return y;

@@ -46,13 +46,18 @@ void HipTensor::uploadFrom(const Tensor& src) {
 }
 
 Tensor HipTensor::download() const {
+  if (shape_.empty()) return Tensor();
   Tensor out(shape_, 0.0f);
   downloadTo(out);
   return out;
 }
 
+// A host tensor of another shape is an error, as CudaTensor::downloadTo
+// (src/cuda_tensor.cc:88-95): nothing is reallocated behind the caller.
 void HipTensor::downloadTo(Tensor& dst) const {
-  if (dst.shape != shape_) dst = Tensor(shape_, 0.0f);
+  if (dst.shape != shape_)
+    throw std::runtime_error("HipTensor::downloadTo shape mismatch: device=" + shapeString() +
+                             " host=" + dst.shapeString());
   buffer_.download(dst.data.data(), numel_ * sizeof(float));
 }
 

@@ -143,6 +143,39 @@ __global__ __launch_bounds__(256) void eltwise_kernel(const float* __restrict__ 
   }
 }
 
+// ---- softmax ----------------------------------------------------------------------
+// y = exp(x - max) / sum over one vector (softmax, src/ops.cc:74-109;
+// cudaSoftmax, src/cuda_ops.cu:567-600): one workgroup, three passes over x
+// (max, then exp and sum, then the division); the fp32 sum is a tree, not
+// the CPU's sequential one.
+constexpr int kSoftmaxThreads = 1024;
+__global__ __launch_bounds__(kSoftmaxThreads) void softmax_kernel(const float* __restrict__ x,
+                                                                  float* __restrict__ y,
+                                                                  int64_t n) {
+  __shared__ float part[kSoftmaxThreads / 64];
+  const int tid = threadIdx.x;
+  auto block_reduce = [&](float v, bool is_max) {
+    v = is_max ? wave_max(v) : wave_sum(v);
+    __syncthreads();
+    if ((tid & 63) == 0) part[tid >> 6] = v;
+    __syncthreads();
+    float r = part[0];
+    for (int i = 1; i < kSoftmaxThreads / 64; ++i) r = is_max ? fmaxf(r, part[i]) : r + part[i];
+    return r;
+  };
+  float mx = -INFINITY;
+  for (int64_t i = tid; i < n; i += kSoftmaxThreads) mx = fmaxf(mx, x[i]);
+  mx = block_reduce(mx, true);
+  float sum = 0.0f;
+  for (int64_t i = tid; i < n; i += kSoftmaxThreads) {
+    const float e = expf(x[i] - mx);
+    y[i] = e;
+    sum += e;
+  }
+  sum = block_reduce(sum, false);
+  for (int64_t i = tid; i < n; i += kSoftmaxThreads) y[i] = y[i] / sum;
+}
+
 // ---- embedding ------------------------------------------------------------------
 // y = table[token] (embeddingLookupKernel, src/cuda_ops.cu:415-421). A device
 // token outside [0, vocab) yields a NaN row instead of a wild read.
@@ -187,6 +220,7 @@ struct RopeArgs {
   float* values;
   int n_heads, n_kv, hd, neox;
   int layer, max_seq;
+  int pos_limit;  // positions >= pos_limit (<= max_seq) write nothing
   const int32_t* pos_dev;
   int pos;
   float theta;
@@ -199,7 +233,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   if (p >= total) return;
   const int pos = read_scalar(a.pos_dev, a.pos);
   const bool cache = a.keys != nullptr;
-  if (cache && (pos < 0 || pos >= a.max_seq)) return;
+  if (cache && (pos < 0 || pos >= a.pos_limit)) return;
   const int head = p / half;
   const int i = p - head * half;
   const int i0 = a.neox ? i : 2 * i;
@@ -342,6 +376,10 @@ struct AttnArgs {
   float* out;           // [n_heads][hd]
   float* part;          // workspace: m, l [n_heads][chunks]; acc [n_heads][chunks][hd]
   int layer, max_seq, n_kv, hd, group, chunks, chunk_len;
+  // Positions at or past pos_limit (the smaller of the cache capacity, the
+  // caller's limit and what `chunks` partials cover) write no cache row and
+  // give NaN outputs.
+  int pos_limit;
   int vec;              // K/V rows are float4-aligned (hd % 4 == 0, aligned cache)
   // Query rows (grid z): row r sits at position pos + r and reads q at
   // q + r * q_stride, writes out + r * out_stride; partials are [rows] x
@@ -397,7 +435,7 @@ __global__ __launch_bounds__(64) void attn_chunk_kernel(AttnArgs a) {
   const int pos = read_scalar(a.pos_dev, a.pos) + qrow;
   const int len = pos + 1;
   const int t0 = blockIdx.x * CH;
-  if (pos < 0 || pos >= a.max_seq || t0 >= len) return;
+  if (pos < 0 || pos >= a.pos_limit || t0 >= len) return;
   const int nt = min(CH, len - t0);
   const int kvh = blockIdx.y;
   const int lane = threadIdx.x;
@@ -542,7 +580,7 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int tb = blockIdx.x * (W * P);  // first position of the workgroup
-  if (pos < 0 || pos >= a.max_seq || tb >= len) return;
+  if (pos < 0 || pos >= a.pos_limit || tb >= len) return;
   const int t0 = tb + wave * P;         // first position of this wave
   const int nt = max(0, min(P, len - t0));  // 0: an idle wave past the end
   const int kvh = blockIdx.y;
@@ -927,7 +965,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   const int head = blockIdx.x;
   const int lane = threadIdx.x;
   float* out = a.out + (size_t)qrow * a.out_stride + (size_t)head * a.hd;
-  if (pos < 0 || pos >= a.max_seq) {  // only reachable through a device position
+  if (pos < 0 || pos >= a.pos_limit) {  // only reachable through a device position
     for (int d = lane; d < a.hd; d += 64) out[d] = __builtin_nanf("");
     return;
   }
@@ -1221,6 +1259,11 @@ hipError_t launch_eltwise(int op, const float* a, const float* b, float* y, int6
   return hipGetLastError();
 }
 
+hipError_t launch_softmax(const float* x, float* y, int64_t n, hipStream_t stream) {
+  hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(kSoftmaxThreads), 0, stream, x, y, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_embedding(const float* table, int vocab, int dim, const int32_t* token_dev,
                             int token, float* y, hipStream_t stream, const RopeTable& rt) {
   const int blocks = (dim + 255) / 256;
@@ -1242,6 +1285,7 @@ hipError_t launch_rope(const RopeLaunch& r, hipStream_t stream) {
   a.neox = r.neox;
   a.layer = r.layer;
   a.max_seq = r.max_seq;
+  a.pos_limit = r.pos_limit > 0 ? std::min(r.pos_limit, r.max_seq) : r.max_seq;
   a.pos_dev = r.pos_dev;
   a.pos = r.pos;
   a.theta = r.theta;
@@ -1369,6 +1413,9 @@ hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   if (r.rope_cs != nullptr && !reg) return hipErrorInvalidValue;
   a.chunk_len = reg ? attn_reg_chunk(r.hd) : kAttnLdsChunk;
   a.chunks = (r.max_len + a.chunk_len - 1) / a.chunk_len;
+  // a row's combine reads pos / chunk_len + 1 partials: at most `chunks`
+  a.pos_limit = std::min(r.max_seq, a.chunks * a.chunk_len);
+  if (r.pos_limit > 0) a.pos_limit = std::min(a.pos_limit, r.pos_limit);
   a.pos_dev = r.pos_dev;
   a.pos = r.pos;
   a.scale = sqrtf(1.0f / (float)r.hd);

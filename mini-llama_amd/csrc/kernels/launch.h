@@ -136,6 +136,8 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 enum { kEltAdd = 0, kEltMul = 1, kEltSilu = 2, kEltSwiGLU = 3 };
 hipError_t launch_eltwise(int op, const float* a, const float* b, float* y, int64_t n,
                           hipStream_t stream);
+// softmax of one vector of n floats (one workgroup).
+hipError_t launch_softmax(const float* x, float* y, int64_t n, hipStream_t stream);
 // token_dev (device int32, may be null) overrides token. With rt.cs
 // non-null the launch also writes the step's RoPE table (cos of pair i at
 // cs[i], sin at cs[hd/2 + i]) for position pos (pos_dev overrides).
@@ -159,6 +161,8 @@ struct RopeLaunch {
   float* values = nullptr;
   int n_heads = 0, n_kv = 0, hd = 0, neox = 0;
   int layer = 0, max_seq = 0;
+  // positions at or past pos_limit write no cache row (0: max_seq)
+  int pos_limit = 0;
   const int32_t* pos_dev = nullptr;
   int pos = 0;
   float theta = 10000.0f;
@@ -177,6 +181,9 @@ struct AttnLaunch {
   float* ws = nullptr;
   int layer = 0, max_seq = 0, n_heads = 0, n_kv = 0, hd = 0;
   int max_len = 0;
+  // A position at or past pos_limit (0: no limit beyond the cache capacity
+  // and max_len) writes no cache row and gives NaN outputs.
+  int pos_limit = 0;
   const int32_t* pos_dev = nullptr;
   int pos = 0;
   // Fused RoPE + cache write of position pos (attention_fusable shapes):

@@ -98,7 +98,10 @@ def _upload_gate_up(gate: dict, up: dict, device) -> TiledWeight:
 class DecodeModel:
     """A model resident on one device with its KV cache and workspace."""
 
-    def __init__(self, model: dict, device: str = "cuda", fuse: bool = True):
+    def __init__(self, model: dict, device: str = "cuda", fuse: bool = True,
+                 cache_len: int | None = None):
+        """cache_len: KV-cache capacity in positions (default and minimum:
+        the model's max_seq_len)."""
         import torch
         c = dict(model["config"])
         c.setdefault("head_dim", c["dim"] // c["n_heads"])
@@ -171,11 +174,12 @@ class DecodeModel:
         _check(lib().mlq_decode_workspace(ctypes.byref(m), ctypes.byref(nbytes)),
                "mlq_decode_workspace")
         self.workspace = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
-        shape = (n_layers, c["max_seq_len"], c["n_kv_heads"], hd)
+        cap = max(int(cache_len or 0), c["max_seq_len"])
+        shape = (n_layers, cap, c["n_kv_heads"], hd)
         self.keys = torch.zeros(shape, dtype=torch.float32, device=self.device)
         self.values = torch.zeros(shape, dtype=torch.float32, device=self.device)
         self._cache = MlqKvCache(self.keys.data_ptr(), self.values.data_ptr(), n_layers,
-                                 c["max_seq_len"], c["n_kv_heads"], hd)
+                                 cap, c["n_kv_heads"], hd)
         self.logits = torch.empty(c["vocab_size"], dtype=torch.float32, device=self.device)
         self.token_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.pos_dev = torch.zeros(1, dtype=torch.int32, device=self.device)

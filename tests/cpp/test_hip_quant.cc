@@ -17,10 +17,15 @@
 #include <vector>
 
 #include "mini_llama/backend.h"
+#include "mini_llama/hip_attention.h"
+#include "mini_llama/hip_kv_cache.h"
+#include "mini_llama/hip_matmul.h"
+#include "mini_llama/hip_ops.h"
 #include "mini_llama/hip_quant.h"
 #include "mini_llama/hip_runtime.h"
 #include "mini_llama/hip_tensor.h"
 #include "mini_llama/hip_weight_upload.h"
+#include "forward_ref.h"
 #include "quant_ref.h"
 
 using namespace mini_llama;
@@ -313,6 +318,176 @@ TEST(hip_uploaded_weight_matches_aos_pointer) {
   CHECK(expectNear(via_registry, via_aos, 0.0f, "registry vs aos (bit-exact)"));
   CHECK(expectNear(via_uploaded, via_aos, 0.0f, "uploaded vs aos (bit-exact)"));
   CHECK(expectNear(via_aos, cpu, 1e-4f, "aos vs cpu"));
+  return true;
+}
+
+// ---- F32 projections: hipLinearUploaded runs them as forwardLinearDevice does
+// (src/forward.cc:206-209, cudaLinearDeviceInput) ------------------------------
+TEST(hip_uploaded_f32_weight_matches_cpu) {
+  SKIP_WITHOUT_HIP();
+  std::mt19937 rng(77);
+  std::uniform_real_distribution<float> u(-1.0f, 1.0f);
+  const int n = 37, k = 70;
+  Tensor w({n, k});
+  for (auto& v : w.data) v = u(rng);
+  QuantizedTensor qt;
+  qt.type = QuantType::kF32;
+  qt.shape = {n, k};
+  qt.f32_data = w.data;
+  HipModelWeights storage;
+  uploadLinearWeight(storage, qt, "layers.0.wo", 0);
+  const HipUploadedWeight* up = findHipWeight(storage, "layers.0.wo", QuantType::kF32);
+  CHECK(up != nullptr);
+  for (int rows : {1, 3, 9}) {
+    Tensor x({rows, k});
+    for (auto& v : x.data) v = u(rng);
+    Tensor got = hipLinearUploaded(hipTensorFromHost(x, 0), *up, 0).download();
+    Tensor want({rows, n});
+    for (int r = 0; r < rows; ++r)
+      ref_linear_f32(x.data.data() + (size_t)r * k, w.data.data(), want.data.data() + (size_t)r * n,
+                     n, k);
+    CHECK(expectNear(got, want, 1e-4f, "uploaded F32 vs linearNaive"));
+    // the host and device F32 entry points agree with it
+    CHECK(expectNear(hipLinear(x, w), want, 1e-4f, "hipLinear"));
+    CHECK(expectNear(hipLinearDeviceWeight(x, up->buffer.data(), qt.shape), want, 1e-4f,
+                     "hipLinearDeviceWeight"));
+  }
+  // 1-D input keeps a 1-D output (cuda_matmul.cc:223-226)
+  Tensor x1({k});
+  for (auto& v : x1.data) v = u(rng);
+  HipTensor y1 = hipLinearDeviceInput(hipTensorFromHost(x1, 0), up->buffer.data(), qt.shape, 0);
+  CHECK(y1.shape() == std::vector<int>{n});
+  CHECK(throwsAs<std::runtime_error>([&] {
+    (void)hipLinearDeviceInput(hipTensorFromHost(x1, 0), up->buffer.data(), {n, k + 1}, 0);
+  }));
+  CHECK(throwsAs<std::runtime_error>(
+      [&] { (void)hipLinearDeviceInput(hipTensorFromHost(x1, 0), nullptr, qt.shape, 0); }));
+  return true;
+}
+
+// ---- cudaMatmul's contract: c = a @ b (tests/test_cuda.cc matmul cases) ----
+TEST(hip_matmul_matches_cpu) {
+  SKIP_WITHOUT_HIP();
+  Tensor a({3, 5}), b({5, 4});
+  fillLinear(a, 0.1f, -0.7f);
+  fillLinear(b, 0.05f, -0.5f);
+  Tensor c = hipMatmul(a, b);
+  Tensor want({3, 4});
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 4; ++j) {
+      double s = 0.0;
+      for (int t = 0; t < 5; ++t) s += (double)a.at2(i, t) * b.at2(t, j);
+      want.at2(i, j) = (float)s;
+    }
+  CHECK(expectNear(c, want, 1e-5f, "hipMatmul"));
+  CHECK(throwsAs<std::runtime_error>([&] { (void)hipMatmul(a, a); }));
+  return true;
+}
+
+// ---- the operators against the oracle (ops.cc restatements) ----------------
+TEST(hip_ops_match_cpu) {
+  SKIP_WITHOUT_HIP();
+  Tensor x({33}), w({33}), b({33});
+  fillLinear(x, 0.11f, -1.7f);
+  fillLinear(w, 0.03f, 0.4f);
+  fillLinear(b, -0.07f, 0.9f);
+  Tensor want(x.shape);
+  ref_rmsnorm(x.data.data(), w.data.data(), want.data.data(), 33, 1e-5f);
+  CHECK(expectNear(hipRmsNorm(x, w, 1e-5f), want, 1e-5f, "hipRmsNorm"));
+  HipTensor xd = hipTensorFromHost(x, 0), bd = hipTensorFromHost(b, 0);
+  CHECK(expectNear(hipRmsNormDeviceInput(xd, w, 1e-5f).download(), want, 1e-5f,
+                   "hipRmsNormDeviceInput"));
+  ref_softmax(x.data.data(), want.data.data(), 33);
+  CHECK(expectNear(hipSoftmax(x), want, 1e-6f, "hipSoftmax"));
+  for (size_t i = 0; i < x.size(); ++i) want.data[i] = x.data[i] / (1.0f + std::exp(-x.data[i]));
+  CHECK(expectNear(hipSilu(x), want, 1e-6f, "hipSilu"));
+  CHECK(expectNear(hipSiluDeviceInput(xd).download(), want, 1e-6f, "hipSiluDeviceInput"));
+  for (size_t i = 0; i < x.size(); ++i) want.data[i] = x.data[i] * b.data[i];
+  CHECK(expectNear(hipElementwiseMul(x, b), want, 0.0f, "hipElementwiseMul"));
+  CHECK(expectNear(hipElementwiseMulDeviceInput(xd, bd).download(), want, 0.0f, "mul device"));
+  for (size_t i = 0; i < x.size(); ++i) want.data[i] = x.data[i] + b.data[i];
+  CHECK(expectNear(hipElementwiseAdd(x, b), want, 0.0f, "hipElementwiseAdd"));
+  CHECK(expectNear(hipElementwiseAddDeviceInput(xd, bd).download(), want, 0.0f, "add device"));
+  CHECK(expectNear(hipElementwiseAddDeviceWeight(xd, bd.data(), b.shape).download(), want, 0.0f,
+                   "add device weight"));
+  CHECK(throwsAs<std::runtime_error>([&] { (void)hipRmsNorm(x, w, 0.0f); }));
+  CHECK(throwsAs<std::runtime_error>([&] { (void)hipElementwiseAdd(x, Tensor({32})); }));
+  // embedding row and its range check
+  Tensor table({5, 33});
+  fillLinear(table, 0.01f, -0.2f);
+  HipTensor td = hipTensorFromHost(table, 0);
+  Tensor row = hipEmbeddingLookupDeviceWeight(td.data(), table.shape, 3).download();
+  for (int i = 0; i < 33; ++i) CHECK(row.data[i] == table.at2(3, i));
+  CHECK(throwsAs<std::out_of_range>(
+      [&] { (void)hipEmbeddingLookupDeviceWeight(td.data(), table.shape, 5); }));
+  // RoPE host and device forms against the oracle, both pairings
+  for (RopeType rt : {RopeType::kNormal, RopeType::kNeoX}) {
+    Tensor q({4, 8}), k({2, 8});
+    fillLinear(q, 0.05f, -0.8f);
+    fillLinear(k, -0.04f, 0.6f);
+    Tensor qw = q, kw = k;
+    CHECK(ref_rope(qw.data.data(), kw.data.data(), 4, 2, 8, 7, 10000.0f,
+                   rt == RopeType::kNeoX ? 1 : 0) == 0);
+    Tensor qh = q, kh = k;
+    hipRope(qh, kh, 7, 10000.0f, rt);
+    CHECK(expectNear(qh, qw, 2e-6f, "hipRope q"));
+    CHECK(expectNear(kh, kw, 2e-6f, "hipRope k"));
+    HipTensor qd = hipTensorFromHost(q, 0), kd = hipTensorFromHost(k, 0);
+    hipRopeDeviceInput(qd, kd, 4, 2, 8, 7, 10000.0f, rt);
+    CHECK(expectNear(qd.download(), qw, 2e-6f, "hipRopeDeviceInput q"));
+  }
+  return true;
+}
+
+// ---- KV cache + decode attention (tests/test_cuda.cc:962-1141 style) --------
+TEST(hip_kv_cache_and_attention_match_cpu) {
+  SKIP_WITHOUT_HIP();
+  const int layers = 2, seq = 16, nkv = 2, hd = 8, nh = 4;
+  HipKvCache cache(layers, seq, nkv, hd, 0);
+  CHECK(!cache.empty());
+  CHECK(cache.bytes() == (size_t)2 * layers * seq * nkv * hd * 4);
+  std::vector<float> keys((size_t)layers * seq * nkv * hd, 0.0f), values(keys.size(), 0.0f);
+  std::mt19937 rng(5);
+  std::uniform_real_distribution<float> u(-1.0f, 1.0f);
+  for (int p = 0; p < 5; ++p) {
+    Tensor k({nkv, hd}), v({nkv, hd});
+    for (auto& e : k.data) e = u(rng);
+    for (auto& e : v.data) e = u(rng);
+    if (p % 2 == 0) {
+      cache.write(1, p, k, v);
+    } else {
+      HipTensor kd = hipTensorFromHost(k, 0), vd = hipTensorFromHost(v, 0);
+      cache.writeDevice(1, p, kd, vd);
+    }
+    std::copy(k.data.begin(), k.data.end(), keys.begin() + ((size_t)(seq + p) * nkv * hd));
+    std::copy(v.data.begin(), v.data.end(), values.begin() + ((size_t)(seq + p) * nkv * hd));
+    CHECK(expectNear(cache.readKey(1, p), k, 0.0f, "readKey"));
+    Tensor vh({hd});
+    std::copy(v.data.begin() + hd, v.data.end(), vh.data.begin());
+    CHECK(expectNear(cache.readValueHead(1, p, 1), vh, 0.0f, "readValueHead"));
+  }
+  Tensor q({nh, hd});
+  for (auto& e : q.data) e = u(rng);
+  Tensor want({nh, hd});
+  ref_attention(q.data.data(), keys.data(), values.data(), 1, 4, nh, nkv, hd, seq,
+                want.data.data());
+  CHECK(expectNear(hipAttentionDecode(q, cache, 1, 4, nh, nkv, hd), want, 1e-5f,
+                   "hipAttentionDecode"));
+  HipTensor qd = hipTensorFromHost(q, 0);
+  Tensor got = hipAttentionDecodeDeviceInput(qd, cache, 1, 4, nh, nkv, hd).download();
+  got.shape = {nh, hd};
+  CHECK(expectNear(got, want, 1e-5f, "hipAttentionDecodeDeviceInput"));
+  CHECK(throwsAs<std::out_of_range>([&] { (void)cache.readKey(2, 0); }));
+  CHECK(throwsAs<std::out_of_range>([&] { (void)cache.readKey(0, seq); }));
+  CHECK(throwsAs<std::out_of_range>([&] { (void)hipAttentionDecode(q, cache, 1, seq, nh, nkv, hd); }));
+  CHECK(throwsAs<std::runtime_error>([&] { (void)hipAttentionDecode(q, cache, 1, 4, 3, nkv, hd); }));
+  // downloadTo into a host tensor of another shape throws
+  // (CudaTensor::downloadTo, src/cuda_tensor.cc:88-95)
+  Tensor wrong({3});
+  CHECK(throwsAs<std::runtime_error>([&] { qd.downloadTo(wrong); }));
+  CHECK(wrong.shape == std::vector<int>{3});
+  cache.clear();
+  CHECK(expectNear(cache.readKey(1, 0), Tensor({nkv, hd}), 0.0f, "cleared"));
   return true;
 }
 

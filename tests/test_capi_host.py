@@ -44,7 +44,17 @@ def test_cpp_host_library_exports_reference_interface(pkg):
             assert f"mini_llama::hip{t}{suffix}(" in out, (t, suffix)
     for name in ("uploadLinearWeight", "uploadQ40LinearWeight", "findHipWeight",
                  "HipDeviceBuffer::upload", "hipTensorFromHost",
-                 "parseBackendKind", "hipLinearUploaded", "lookupTiledWeight"):
+                 "parseBackendKind", "hipLinearUploaded", "lookupTiledWeight",
+                 # cuda_matmul.h / cuda_ops.h / cuda_kv_cache.h / cuda_attention.h twins
+                 "hipMatmul(", "hipLinear(", "hipLinearDeviceWeight(", "hipLinearDeviceInput(",
+                 "hipRmsNorm(", "hipRmsNormDeviceWeight(", "hipRmsNormDeviceInput(",
+                 "hipSilu(", "hipSiluDeviceInput(", "hipElementwiseMul(",
+                 "hipElementwiseMulDeviceInput(", "hipElementwiseAdd(",
+                 "hipElementwiseAddDeviceInput(", "hipElementwiseAddDeviceWeight(",
+                 "hipSoftmax(", "hipEmbeddingLookupDeviceWeight(", "hipRope(",
+                 "hipRopeDeviceInput(", "HipKvCache::write(", "HipKvCache::writeDevice(",
+                 "HipKvCache::readKeyHead(", "HipKvCache::clear(",
+                 "hipAttentionDecode(", "hipAttentionDecodeDeviceInput("):
         assert f"mini_llama::{name}" in out, name
 
 

@@ -223,8 +223,10 @@ def test_attention_reference_cases(pkg, oracle, cuda):
     (32, 2, 100, 300, 150), (64, 4, 64, 200, 129),
     # seven query heads per kv head (padded to eight in the kernels)
     (14, 2, 64, 300, 200), (7, 1, 256, 200, 150), (21, 3, 96, 100, 60),
-    # more than 128 chunk partials per head (the combine's register-held
-    # maxima and sums overflow into reads from memory)
+    # more than 128 chunk partials per head: the combine's online max/sum
+    # runs over several chunks per lane, and its weighted sum over more than
+    # one 32-chunk batch (the first batch from the maxima pass, later ones
+    # reloaded)
     (8, 2, 128, 9100, 9000), (6, 3, 96, 4600, 4500)])
 def test_attention_matches_oracle(pkg, oracle, cuda, n_heads, n_kv, hd, max_seq, pos):
     rng = np.random.default_rng(pos * 7 + hd)
@@ -530,6 +532,32 @@ def test_device_position_out_of_range_gives_nan(pkg, cuda):
         dm.pos_dev.fill_(2)
         dm.step_device()
         assert np.isnan(dm.logits.cpu().numpy()).all(), token
+
+
+@pytest.mark.parametrize("qtype", ["q8_0", "q4_0"])
+def test_device_position_past_model_in_larger_cache_gives_nan(pkg, cuda, qtype):
+    """A cache with more positions than the model (the API allows it): a
+    device position at or past the model's max_seq_len gives NaN logits and
+    writes no cache row (forwardToken rejects pos >= max_seq_len,
+    src/forward.cc:42), though the cache could hold the row."""
+    import mini_llama_amd.decode as dec
+    import mini_llama_amd.synth as synth
+    # head_dim 128 (register attention kernel, fused RoPE) and 48 (LDS kernel)
+    for dim, n_heads in ((256, 2), (96, 2)):
+        cfg = dict(vocab_size=64, dim=dim, hidden_dim=128, n_layers=2, n_heads=n_heads,
+                   n_kv_heads=1, max_seq_len=70)
+        dm = dec.DecodeModel(synth.synthetic_model(cfg, qtype, seed=3), cache_len=300)
+        for pos in (70, 71, 127, 128, 200, 299):
+            dm.token_dev.fill_(5)
+            dm.pos_dev.fill_(pos)
+            dm.step_device()
+            assert np.isnan(dm.logits.cpu().numpy()).all(), (dim, pos)
+        assert not dm.keys.cpu().numpy().any() and not dm.values.cpu().numpy().any()
+        # the last position inside the model still works and writes its row
+        dm.pos_dev.fill_(69)
+        dm.step_device()
+        assert np.isfinite(dm.logits.cpu().numpy()).all()
+        assert dm.keys[:, 69].abs().sum().item() > 0 and not dm.keys[:, 70:].any().item()
 
 
 def test_decode_host_validation(pkg, cuda):
