@@ -23,7 +23,9 @@ greedy sampling as one HIP graph, in tokens/s and algorithmic GB/s (weights
 Profiling modes (one kernel family per run, for rocprofv3 counter passes):
 `--mode headline` launches only the headline GEMV (eagerly with `--eager`),
 `--mode copy` runs a plain device-to-device copy of 256 MiB, the known-size
-reference that scales the FETCH_SIZE / WRITE_SIZE counters to bytes.
+reference that scales the FETCH_SIZE / WRITE_SIZE counters to bytes;
+`--mode case --case qtype,m,n,k` launches one Linear shape (the skinny and
+prefill GEMM counter summaries in profiles/ come from it).
 `roofline.traffic` is read from profiles/hbm_traffic_gemv_q4_0_c1.md (the
 summary of those counter runs) when it is present, else null.
 """
@@ -403,8 +405,10 @@ def main():
                     help="also run the decode sweeps and the GGUF upload timing")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--mode", choices=["full", "headline", "copy", "decode"],
-                    default="full", help="headline/copy/decode: profiling runs")
+    ap.add_argument("--mode", choices=["full", "headline", "copy", "decode", "case"],
+                    default="full", help="headline/copy/decode/case: profiling runs")
+    ap.add_argument("--case", default="q4_0,16,4096,4096",
+                    help="--mode case: qtype,m,n,k of the one shape to launch")
     ap.add_argument("--context", type=int, default=1024,
                     help="first position of the timed decode steps")
     ap.add_argument("--eager", action="store_true",
@@ -433,6 +437,12 @@ def main():
     if args.mode == "decode":
         r = bench_decode(pkg, torch, min(args.steps, 200), args.warmup, args.context)
         print(json.dumps({"mode": "decode", **r}), flush=True)
+        return
+    if args.mode == "case":
+        qt, m, n, k = args.case.split(",")
+        r = bench_case(pkg, torch, qt, int(m), int(n), int(k), args.steps, args.warmup,
+                       seed=100, eager=args.eager)
+        print(json.dumps({"mode": "case", **r}), flush=True)
         return
     head = bench_case(pkg, torch, "q4_0", 1, 18944, 3584, args.steps,
                       args.warmup, seed=1000, eager=args.eager)

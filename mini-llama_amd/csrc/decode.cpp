@@ -153,11 +153,10 @@ struct PrefillBuffers {
   float* apart;     // attention partials for kPrefillAttnRows rows
   void* lin;        // Linear workspace for n rows (and 1 row)
   size_t lin_bytes;
-  // n > kSkinnyMaxRows (prefill GEMM): fp16 GEMM inputs written by their
-  // producers (RMSNorm rows, the gate|up SwiGLU epilogue)
+  // n > kSkinnyMaxRows (prefill GEMM): the fp16 GEMM input written by the
+  // RMSNorm producer, with its row exponents
   _Float16* xh;     // [n][f16_row_stride(dim)]
-  _Float16* gh;     // [n][f16_row_stride(hidden)]
-  _Float16* ah;     // [n][f16_row_stride(n_heads * head_dim)] (attention output)
+  int* xexp;        // [n]
   size_t total;
 };
 
@@ -212,8 +211,7 @@ int plan_prefill(const mlq_model* m, int n, char* base, PrefillBuffers* b) {
   b->lin = take(lin);
   const bool gemm_rows = n > kSkinnyMaxRows;
   b->xh = gemm_rows ? (_Float16*)take(rows * f16_row_stride(dim) * 2) : nullptr;
-  b->gh = gemm_rows ? (_Float16*)take(rows * f16_row_stride(hid) * 2) : nullptr;
-  b->ah = gemm_rows ? (_Float16*)take(rows * f16_row_stride(qd) * 2) : nullptr;
+  b->xexp = gemm_rows ? (int*)take(rows * sizeof(int)) : nullptr;
   b->total = off;
   return MLQ_OK;
 }
@@ -549,30 +547,23 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
                     int act) {
     return mlq_linear_epi(&w, x, y, rows, bias, act, b.lin, b.lin_bytes, stream);
   };
-  // Prefill GEMM rows (n > 64, quantized weights): the producers write the
-  // GEMMs' fp16 inputs directly (RMSNorm rows, the SwiGLU epilogue) and the
-  // o / down projections add the residual in their epilogue, which removes
-  // four fp16 copy passes and two residual passes per layer with the same
-  // roundings and additions (GemmOut).
+  // Prefill GEMM rows (n > 64, quantized weights): the RMSNorm producer
+  // writes the q|k|v and gate|up GEMMs' fp16 input directly (rows scaled by
+  // their power-of-two exponents), and the o / down projections add the
+  // residual in their epilogue, which removes two fp16 copy passes and two
+  // residual passes per layer with the same roundings and additions
+  // (GemmOut). The attention output and the SwiGLU output go through the
+  // GEMMs' own fp16 copy pass, which needs the whole row for its exponent.
   auto gemm_rows = [&](const mlq_weight& w) { return n > kSkinnyMaxRows && w.type != MLQ_F32; };
   auto f16_norm_ok = [&](const float* norm) {
     return dim % 4 == 0 && ((uintptr_t)norm & 15) == 0 && dim <= 16 * 4 * 256;
   };
   // (xh rows are f16_row_stride(w.k) halves: w.k is dim or hidden, checked
   // by plan())
-  auto gemm_f16 = [&](const mlq_weight& w, const _Float16* xh, float* y, const Epilogue& e,
-                      const GemmOut& o) {
-    return hip(launch_gemm_f16(w, xh, y, n, b.lin, b.lin_bytes, s, e, o));
+  auto gemm_f16 = [&](const mlq_weight& w, float* y, const Epilogue& e, const GemmOut& o) {
+    return hip(launch_gemm_f16(w, b.xh, b.xexp, y, n, b.lin, b.lin_bytes, s, e, o));
   };
-  const int ldx = f16_row_stride(dim), ldh = f16_row_stride(hid), ldq = f16_row_stride(qd);
-  // the SwiGLU epilogue and the attention kernel write their columns only;
-  // the GEMMs reading them need zeros up to the padded row length
-  if (n > kSkinnyMaxRows && ldh > hid) {
-    if ((rc = hip(launch_fill_zero(b.gh, (size_t)n * ldh * 2, s))) != MLQ_OK) return rc;
-  }
-  if (n > kSkinnyMaxRows && ldq > qd) {
-    if ((rc = hip(launch_fill_zero(b.ah, (size_t)n * ldq * 2, s))) != MLQ_OK) return rc;
-  }
+  const int ldx = f16_row_stride(dim);
   if ((rc = hip(hipMemcpyAsync(b.tokens, tokens, (size_t)n * sizeof(int32_t),
                                hipMemcpyHostToDevice, s))) != MLQ_OK)
     return rc;
@@ -587,10 +578,11 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
       if (!qkv_f16) return linear(w, b.h, y, n, bias, MLQ_EPI_NONE);
       Epilogue e;
       e.bias = bias;
-      return gemm_f16(w, b.xh, y, e, GemmOut());
+      return gemm_f16(w, y, e, GemmOut());
     };
     if (qkv_f16)
-      rc = hip(launch_rmsnorm_f16(b.x, l.attn_norm, b.xh, n, dim, ldx, m->rms_norm_eps, s));
+      rc = hip(launch_rmsnorm_f16(b.x, l.attn_norm, b.xh, b.xexp, n, dim, ldx, m->rms_norm_eps,
+                                  s));
     else
       rc = hip(launch_rmsnorm(b.x, l.attn_norm, b.h, n, dim, m->rms_norm_eps, s));
     if (rc != MLQ_OK) return rc;
@@ -627,8 +619,6 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
     // kernel over blocks of query rows
     const bool mfma_attn = prefill_attention_supported(hd, m->n_heads / m->n_kv_heads) &&
                            ((uintptr_t)c->keys & 15) == 0 && ((uintptr_t)c->values & 15) == 0;
-    // the attention kernel writes the o projection's fp16 input directly
-    const bool attn_f16 = mfma_attn && gemm_rows(l.wo);
     if (mfma_attn) {
       AttnLaunch a;
       a.q = rr.q;
@@ -643,8 +633,7 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
       a.pos = start_pos;
       a.rows = n;
       a.q_stride = rr.q_stride;
-      a.out_stride = attn_f16 ? ldq : qd;
-      a.out_h = attn_f16 ? b.ah : nullptr;
+      a.out_stride = qd;
       if ((rc = hip(launch_attention_prefill(a, s))) != MLQ_OK) return rc;
     }
     for (int r0 = 0; !mfma_attn && r0 < n; r0 += kPrefillAttnRows) {
@@ -668,11 +657,7 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
       if ((rc = hip(launch_attention(a, s))) != MLQ_OK) return rc;
     }
     // x2 = x + wo . attn (the GEMM adds the residual row by row)
-    if (attn_f16) {
-      GemmOut o;
-      o.residual = b.x;
-      if ((rc = gemm_f16(l.wo, b.ah, b.x2, Epilogue(), o)) != MLQ_OK) return rc;
-    } else if (gemm_rows(l.wo)) {
+    if (gemm_rows(l.wo)) {
       GemmOut o;
       o.residual = b.x;
       if ((rc = hip(launch_gemm_ws(l.wo, b.attn, b.x2, n, b.lin, b.lin_bytes, s, Epilogue(),
@@ -684,22 +669,21 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
         return rc;
     }
     // x = x2 + w_down . swiglu(w_gate . h, w_up . h); with gate|up
-    // interleaved and prefill GEMM rows: fp16 input from RMSNorm, fp16
-    // SwiGLU output from the epilogue, residual in the down GEMM
+    // interleaved and prefill GEMM rows: fp16 input from RMSNorm, the SwiGLU
+    // epilogue in the gate|up GEMM, residual in the down GEMM
     if (glu_fused(l) && gemm_rows(l.w_gate) && gemm_rows(l.w_down) &&
         f16_norm_ok(l.ffn_norm)) {
-      if ((rc = hip(launch_rmsnorm_f16(b.x2, l.ffn_norm, b.xh, n, dim, ldx, m->rms_norm_eps,
-                                       s))) != MLQ_OK)
+      if ((rc = hip(launch_rmsnorm_f16(b.x2, l.ffn_norm, b.xh, b.xexp, n, dim, ldx,
+                                       m->rms_norm_eps, s))) != MLQ_OK)
         return rc;
       Epilogue eg;
       eg.act = kEpiSwiGLU;
-      GemmOut og;
-      og.yh = b.gh;
-      og.yh_ld = ldh;
-      if ((rc = gemm_f16(l.w_gate, b.xh, nullptr, eg, og)) != MLQ_OK) return rc;
+      if ((rc = gemm_f16(l.w_gate, b.ffn, eg, GemmOut())) != MLQ_OK) return rc;
       GemmOut od;
       od.residual = b.x2;
-      if ((rc = gemm_f16(l.w_down, b.gh, b.x, Epilogue(), od)) != MLQ_OK) return rc;
+      if ((rc = hip(launch_gemm_ws(l.w_down, b.ffn, b.x, n, b.lin, b.lin_bytes, s, Epilogue(),
+                                   od))) != MLQ_OK)
+        return rc;
       continue;
     }
     if ((rc = hip(launch_rmsnorm(b.x2, l.ffn_norm, b.h, n, dim, m->rms_norm_eps, s))) != MLQ_OK)

@@ -385,9 +385,6 @@ struct AttnArgs {
   // q + r * q_stride, writes out + r * out_stride; partials are [rows] x
   // [n_heads] x [chunks]. One row for a decode step.
   int rows, q_stride, out_stride;
-  // prefill kernel only: with out_h non-null the output rows are written as
-  // fp16 (round to nearest even) at out_h + r * out_stride instead of out
-  _Float16* out_h;
   const int32_t* pos_dev;
   int pos;
   float scale;
@@ -947,8 +944,7 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
       o += macc[(w * 16 + m) * HD + d] * f;
     }
     const size_t at = (size_t)qr * a.out_stride + (size_t)(kvh * G + m % GP) * HD + d;
-    if (a.out_h != nullptr) a.out_h[at] = (_Float16)(o / lsum);
-    else a.out[at] = o / lsum;
+    a.out[at] = o / lsum;
   }
 }
 
@@ -1150,12 +1146,15 @@ __global__ __launch_bounds__(kArgmaxSliceThreads) void argmax_final_kernel(
   }
 }
 
-// rmsnorm_vec_kernel with fp16 output rows of ld halves (zero past dim).
+// rmsnorm_vec_kernel with fp16 output rows of ld halves (zero past dim):
+// row r holds y * 2^rexp[r], rexp[r] = pow2_scale_exp(max |y|) (any finite
+// row fits fp16; the GEMM reading the copy scales its results back).
 template <int R>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_f16_kernel(
     const float* __restrict__ x, const float* __restrict__ w,
-    _Float16* __restrict__ yh, int dim, int ld, float eps) {
+    _Float16* __restrict__ yh, int* __restrict__ rexp, int dim, int ld, float eps) {
   __shared__ float part[kNormThreads / 64];
+  __shared__ float pmax[kNormThreads / 64];
   const int n4 = dim >> 2;
   const f4_t* xr = (const f4_t*)(x + (size_t)blockIdx.x * dim);
   uint2* yr = (uint2*)(yh + (size_t)blockIdx.x * ld);
@@ -1182,13 +1181,29 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_f16_kernel(
 #pragma unroll
   for (int i = 0; i < kNormThreads / 64; ++i) total += part[i];
   const float scale = sqrtf(total / (float)dim + eps);
+  // the normalised row, its largest magnitude, and the row's power-of-two
+  // scale for the fp16 copy (pow2_scale_exp; the GEMM scales back)
+  float mx = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    v[r] = f4_t{v[r].x * wv[r].x / scale, v[r].y * wv[r].y / scale,
+                v[r].z * wv[r].z / scale, v[r].w * wv[r].w / scale};
+    mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[r].x), fabsf(v[r].y))), fmaxf(fabsf(v[r].z), fabsf(v[r].w)));
+  }
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) pmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) mx = fmaxf(mx, pmax[i]);
+  const int e = pow2_scale_exp(mx);
+  if (threadIdx.x == 0) rexp[blockIdx.x] = e;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int i = threadIdx.x + r * kNormThreads;
     if (i < n4) {
       uint2 o;
-      o.x = pack_h2(v[r].x * wv[r].x / scale, v[r].y * wv[r].y / scale);
-      o.y = pack_h2(v[r].z * wv[r].z / scale, v[r].w * wv[r].w / scale);
+      o.x = pack_h2(ldexp_f(v[r].x, e), ldexp_f(v[r].y, e));
+      o.y = pack_h2(ldexp_f(v[r].z, e), ldexp_f(v[r].w, e));
       yr[i] = o;
     }
   }
@@ -1204,18 +1219,18 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(uint32_t* p, size_t n) {
 }  // namespace
 
 // ---- launchers ---------------------------------------------------------------------
-hipError_t launch_rmsnorm_f16(const float* x, const float* w, _Float16* yh, int rows, int dim,
-                              int ld, float eps, hipStream_t stream) {
+hipError_t launch_rmsnorm_f16(const float* x, const float* w, _Float16* yh, int* rexp, int rows,
+                              int dim, int ld, float eps, hipStream_t stream) {
   const bool ok = dim % 4 == 0 && ld % 4 == 0 && ld >= dim && ((uintptr_t)x & 15) == 0 &&
                   ((uintptr_t)w & 15) == 0 && ((uintptr_t)yh & 15) == 0;
   const int per = (dim / 4 + kNormThreads - 1) / kNormThreads;
   if (!ok || per > 16) return hipErrorInvalidValue;
   const dim3 grid(rows), block(kNormThreads);
-  if (per <= 1) hipLaunchKernelGGL(rmsnorm_f16_kernel<1>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
-  else if (per <= 2) hipLaunchKernelGGL(rmsnorm_f16_kernel<2>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
-  else if (per <= 4) hipLaunchKernelGGL(rmsnorm_f16_kernel<4>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
-  else if (per <= 8) hipLaunchKernelGGL(rmsnorm_f16_kernel<8>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
-  else hipLaunchKernelGGL(rmsnorm_f16_kernel<16>, grid, block, 0, stream, x, w, yh, dim, ld, eps);
+  if (per <= 1) hipLaunchKernelGGL(rmsnorm_f16_kernel<1>, grid, block, 0, stream, x, w, yh, rexp, dim, ld, eps);
+  else if (per <= 2) hipLaunchKernelGGL(rmsnorm_f16_kernel<2>, grid, block, 0, stream, x, w, yh, rexp, dim, ld, eps);
+  else if (per <= 4) hipLaunchKernelGGL(rmsnorm_f16_kernel<4>, grid, block, 0, stream, x, w, yh, rexp, dim, ld, eps);
+  else if (per <= 8) hipLaunchKernelGGL(rmsnorm_f16_kernel<8>, grid, block, 0, stream, x, w, yh, rexp, dim, ld, eps);
+  else hipLaunchKernelGGL(rmsnorm_f16_kernel<16>, grid, block, 0, stream, x, w, yh, rexp, dim, ld, eps);
   return hipGetLastError();
 }
 
@@ -1386,7 +1401,6 @@ static void attn_launch_g(const AttnArgs& a, hipStream_t stream) {
 
 hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   AttnArgs a;
-  a.out_h = nullptr;  // (prefill kernel only)
   a.q = r.q;
   a.keys = r.keys;
   a.values = r.values;
@@ -1467,7 +1481,6 @@ hipError_t launch_attention_prefill(const AttnLaunch& r, hipStream_t stream) {
   a.rows = r.rows;
   a.q_stride = r.q_stride;
   a.out_stride = r.out_stride;
-  a.out_h = r.out_h;
   a.scale = sqrtf(1.0f / (float)r.hd);
   if (!prefill_attention_supported(r.hd, a.group) || ((uintptr_t)r.keys & 15) != 0 ||
       ((uintptr_t)r.values & 15) != 0)

@@ -121,6 +121,48 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   return as_u32(h);
 }
 
+// Power-of-two exponent that scales a set of values whose largest magnitude
+// is amax into [2^14, 2^15): amax * 2^e lies there (amax zero or not finite:
+// e = 0, values pass through and inf / NaN propagate). fp16 copies (and fp16
+// hi/lo pairs) of x * 2^e then hold any finite fp32 activations without
+// overflow, with the fp16 subnormal floor 2^-39 below the largest element;
+// the fp32 results are scaled back by 2^-e (exact: ldexp).
+__device__ __forceinline__ int pow2_scale_exp(float amax) {
+  if (!(amax > 0.0f) || !(amax <= 3.402823466e38f)) return 0;
+  return 15 - __builtin_amdgcn_frexp_expf(amax);
+}
+__device__ __forceinline__ float ldexp_f(float v, int e) { return __builtin_amdgcn_ldexpf(v, e); }
+__device__ __forceinline__ float abs_max4(float m, float4 v) {
+  return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Largest of a non-negative value over the 64 lanes of a wave, wave-uniform
+// (a scalar register): DPP within each 16-lane row, then the four row
+// results on the scalar unit, compared as integers (non-negative floats
+// order like their bit patterns). No LDS round trips, unlike shuffles.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  int b = __builtin_bit_cast(int, v);
+  b = max(b, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  b = max(b, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  b = max(b, __builtin_amdgcn_mov_dpp(b, 0x124, 0xF, 0xF, false));  // row_ror:4
+  b = max(b, __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));  // row_ror:8
+  const int r = max(max(__builtin_amdgcn_readlane(b, 0), __builtin_amdgcn_readlane(b, 16)),
+                    max(__builtin_amdgcn_readlane(b, 32), __builtin_amdgcn_readlane(b, 48)));
+  return __builtin_bit_cast(float, r);
+}
+
+// Bitwise OR over the 64 lanes of a wave, wave-uniform: DPP within each
+// 16-lane row, then the four row results on the scalar unit.
+__device__ __forceinline__ uint32_t wave_or(uint32_t v) {
+  int b = (int)v;
+  b |= __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  b |= __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  b |= __builtin_amdgcn_mov_dpp(b, 0x124, 0xF, 0xF, false);  // row_ror:4
+  b |= __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false);  // row_ror:8
+  return (uint32_t)(__builtin_amdgcn_readlane(b, 0) | __builtin_amdgcn_readlane(b, 16) |
+                    __builtin_amdgcn_readlane(b, 32) | __builtin_amdgcn_readlane(b, 48));
+}
+
 // Sum / max over the 64 lanes of a wave (every lane gets the result).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -27,8 +27,12 @@
 //  - Workgroups are numbered XCD-major: the m-tiles of one weight column
 //    block run on the same XCD and share its L2.
 //  - With a workspace, x is first converted once to an fp16 copy
-//    (x_to_f16_kernel): the GEMM then moves half the activation bytes per
+//    (row_copy.h): the GEMM then moves half the activation bytes per
 //    stage and does no conversion work. Without one it reads fp32 x.
+//  - Any finite fp32 activations: each row enters the MFMAs as x * 2^e_r
+//    (e_r = pow2_scale_exp of the row's largest |x|: from the fp16 copy's
+//    row exponents, or found by the workgroup before its K loop when it
+//    reads fp32 x), and the epilogue scales row r by 2^-e_r (exact).
 // The scale is applied before the MFMA (per weight), so no per-block fixup
 // of the accumulators is needed; that is what keeps VALU work independent of
 // m (an int8 MFMA variant would need a per-(m, n, block) fp32 fixup).
@@ -39,6 +43,7 @@
 #include "../mlq_layout.h"
 #include "device_common.h"
 #include "launch.h"
+#include "row_copy.h"
 
 namespace mlq {
 namespace {
@@ -59,6 +64,7 @@ struct GemmArgs {
   const uint8_t* mn;
   const float* x;      // fp32 activations [m][k] (XF32 modes)
   const _Float16* xh;  // fp16 activations [m][kp] (XF16 mode, workspace)
+  const int* rexp;     // XF16 mode: row exponents of xh (x[r] * 2^rexp[r])
   float* y;
   float* part;         // split-K partial outputs [splits][m][n] (splits > 1)
   int m, n, k, g, nt;
@@ -134,7 +140,7 @@ __device__ __forceinline__ void load_x(const GemmArgs& a, XStage& st, rsrc_t rx,
 // the fp16 copy is already zero past k).
 template <int XM>
 __device__ __forceinline__ void store_x(const GemmArgs& a, XStage& st,
-                                        _Float16* as, int s, int tid) {
+                                        _Float16* as, int s, int tid, const int* sexp) {
   if (XM == kXF16) {
     const int c = tid & 7;
 #pragma unroll
@@ -161,9 +167,10 @@ __device__ __forceinline__ void store_x(const GemmArgs& a, XStage& st,
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int r = (tid >> 4) + 16 * j;
+    const int e = sexp[r];  // the row's power-of-two scale
     uint2 hv;
-    hv.x = pack_h2(st.xa[j].x, st.xa[j].y);
-    hv.y = pack_h2(st.xa[j].z, st.xa[j].w);
+    hv.x = pack_h2(ldexp_f(st.xa[j].x, e), ldexp_f(st.xa[j].y, e));
+    hv.y = pack_h2(ldexp_f(st.xa[j].z, e), ldexp_f(st.xa[j].w, e));
     *(uint2*)(as + r * kStride + 4 * c) = hv;
   }
 }
@@ -255,13 +262,14 @@ struct Slot { static constexpr int v = N; };
 // stage s+2 requested in k step 0 of stage s, stored in its last), which
 // wins only when the grid has more workgroups than CUs (3-8 %; 2-8 % slower
 // on smaller grids), so the launcher picks it by grid size.
-// EXT: the output epilogue also applies GemmOut.residual / GemmOut.yh
-// (a separate instantiation: their per-element branches grow the store code
-// of every kernel by half, which measured 3-6 % slower main loops).
+// EXT: the output epilogue also adds GemmOut.residual (a separate
+// instantiation: per-element branches in the store code of every kernel
+// measured 3-6 % slower main loops).
 template <int QT, int XM, int OCC = 1, int XS = 2, bool EXT = false>
 __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
   constexpr int kXS = XS;  // activation register slots (1 or 2)
   __shared__ __align__(16) _Float16 as_buf[3][kBM * kStride];
+  __shared__ __align__(16) int sexp[kBM];  // row exponents of the m tile
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -295,6 +303,29 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
   const rsrc_t rd = make_rsrc(a.d + (size_t)tile0 * a.g * 128, sbytes);
   const rsrc_t rm = QT == MLQ_Q4_1 ? make_rsrc(a.mn + (size_t)tile0 * a.g * 128, sbytes) : rd;
 
+  // Row exponents of the tile's rows: from the fp16 copy, or (fp32 x) from
+  // the rows' largest |x| over all of K, 16 threads per row
+  if constexpr (XM == kXF16) {
+    if (tid < kBM) sexp[tid] = tid < rows ? a.rexp[m0 + tid] : 0;
+  } else {
+    const int c = tid & 15;
+    for (int r = tid >> 4; r < kBM; r += kThreads / 16) {
+      float mx = 0.0f;
+      if (r < rows) {
+        const float* xr = a.x + (size_t)(m0 + r) * a.k;
+        if (XM == kXF32Vec) {
+          for (int kk = 4 * c; kk < a.k; kk += 64) mx = abs_max4(mx, *(const float4*)(xr + kk));
+        } else {
+          for (int kk = c; kk < a.k; kk += 16) mx = fmaxf(mx, fabsf(xr[kk]));
+        }
+      }
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      if (c == 0) sexp[r] = pow2_scale_exp(mx);
+    }
+  }
+  __syncthreads();
+
   f16v_t acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -311,7 +342,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
     load_w<QT>(a, st, rq, rd, rm, sbase + rel, lane, wn);
   };
   auto sx = [&](XStage& st, int slab, int rel) {
-    store_x<XM>(a, st, as_buf[slab], sbase + rel, tid);
+    store_x<XM>(a, st, as_buf[slab], sbase + rel, tid, sexp);
   };
   // fragment rows of this lane: MFMA operand row/col = lane % 32, k octet
   // = lane / 32
@@ -414,8 +445,24 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
   if (s + 4 <= stages) { step(s + 2, Slot<2>{}); step(s + 3, Slot<3>{}); }
 
   // epilogue: lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each
-  // 32x32 block; with several K ranges each writes its own raw partial
-  // slice and the reduce applies the epilogue
+  // 32x32 block; first every row is scaled back by 2^-e of its exponent
+  // (four consecutive rows per 16-byte LDS read)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int4 e4 = *(const int4*)(sexp + 32 * i + 8 * q + 4 * (lane >> 5));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        acc[i][j][4 * q + 0] = ldexp_f(acc[i][j][4 * q + 0], -e4.x);
+        acc[i][j][4 * q + 1] = ldexp_f(acc[i][j][4 * q + 1], -e4.y);
+        acc[i][j][4 * q + 2] = ldexp_f(acc[i][j][4 * q + 2], -e4.z);
+        acc[i][j][4 * q + 3] = ldexp_f(acc[i][j][4 * q + 3], -e4.w);
+      }
+    }
+  }
+  // with several K ranges each writes its own raw partial slice and the
+  // reduce applies the epilogue
   if (a.splits > 1) {
     float* out = a.part + (size_t)sp * a.m * a.n;
 #pragma unroll
@@ -433,16 +480,11 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
     }
     return;
   }
-  // output (mrow, col) of y [m][ny]: + residual, fp32 or fp16 store
+  // output (mrow, col) of y [m][ny] (+ residual)
   auto put = [&](int mrow, int col, float o) {
     const size_t idx = (size_t)mrow * a.ny + col;
-    if constexpr (EXT) {
-      if (a.out.residual != nullptr) o += a.out.residual[idx];
-      if (a.out.yh != nullptr) a.out.yh[(size_t)mrow * a.out.yh_ld + col] = (_Float16)o;
-      else a.y[idx] = o;
-    } else {
-      a.y[idx] = o;
-    }
+    if constexpr (EXT) o += a.out.residual[idx];
+    a.y[idx] = o;
   };
   // one code path per (bias, SwiGLU) choice: no per-element branches; the
   // bias depends on the column only, so a lane loads it once per block
@@ -526,43 +568,11 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, fl
 #pragma unroll
     for (int e = 0; e < V; ++e) out[e] += go.residual[o + e];
   }
-  if (go.yh != nullptr) {
-    _Float16* yr = go.yh + (size_t)r * go.yh_ld + c;
-#pragma unroll
-    for (int e = 0; e < V; ++e) yr[e] = (_Float16)out[e];
-  } else if (VEC) {
+  if (VEC) {
     *(float4*)(y + o) = make_float4(out[0], out[V > 1 ? 1 : 0], out[V > 2 ? 2 : 0], out[V > 3 ? 3 : 0]);
   } else {
     y[o] = out[0];
   }
-}
-
-// x fp32 [m][k] -> fp16 [m][kp], zero for k <= col < kp. One thread per 8
-// output halves (one 16-byte store).
-__global__ __launch_bounds__(256) void x_to_f16_kernel(const float* x,
-                                                       _Float16* xh, int m,
-                                                       int k, int kp) {
-  const int per_row = kp / 8;
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)m * per_row) return;
-  const int r = (int)(idx / per_row), c0 = (int)(idx % per_row) * 8;
-  const float* xr = x + (size_t)r * k;
-  float v[8];
-  if ((k & 3) == 0 && c0 + 8 <= k) {
-    const float4 lo = *(const float4*)(xr + c0);
-    const float4 hi = *(const float4*)(xr + c0 + 4);
-    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = c0 + e < k ? xr[c0 + e] : 0.0f;
-  }
-  uint4 o;
-  o.x = pack_h2(v[0], v[1]);
-  o.y = pack_h2(v[2], v[3]);
-  o.z = pack_h2(v[4], v[5]);
-  o.w = pack_h2(v[6], v[7]);
-  *(uint4*)(xh + (size_t)r * kp + c0) = o;
 }
 
 template <int QT, bool EXT>
@@ -578,13 +588,14 @@ void launch_f16(const GemmArgs& a, unsigned grid, hipStream_t stream) {
 template <int QT>
 hipError_t launch_typed(const GemmArgs& a, int xm, hipStream_t stream) {
   const unsigned grid = (unsigned)(a.mtiles * a.ntiles * a.splits);
-  // residual / fp16 output in the GEMM's own store (split K: the reduce
-  // applies them); the prefill paths that set them read the fp16 copy
-  const bool ext = a.splits == 1 && (a.out.residual != nullptr || a.out.yh != nullptr);
+  // residual in the GEMM's own store (split K: the reduce adds it); the
+  // prefill paths that set it read the fp16 copy
+  const bool ext = a.splits == 1 && a.out.residual != nullptr;
   if (ext && xm != kXF16) return hipErrorInvalidValue;
   switch (xm) {
     case kXF32Vec: gemm_kernel<QT, kXF32Vec><<<grid, kThreads, 0, stream>>>(a); break;
-    case kXF32Scalar: gemm_kernel<QT, kXF32Scalar><<<grid, kThreads, 0, stream>>>(a); break;
+    // (element-wise loads: one activation register slot keeps it spill-free)
+    case kXF32Scalar: gemm_kernel<QT, kXF32Scalar, 1, 1><<<grid, kThreads, 0, stream>>>(a); break;
     default:
       if (ext) launch_f16<QT, true>(a, grid, stream);
       else launch_f16<QT, false>(a, grid, stream);
@@ -633,7 +644,14 @@ hipError_t launch_split_reduce(const float* part, float* y, int m, int n, int sp
 // every stage (GEMM) and group (skinny GEMM) of a row stays inside it.
 int f16_row_stride(int k) { return (k + kGroupK - 1) / kGroupK * kGroupK; }
 
-size_t f16_copy_bytes(int m, int k) { return (size_t)m * f16_row_stride(k) * 2; }
+// the fp16 rows, then the row exponents
+size_t f16_copy_bytes(int m, int k) {
+  return align256((size_t)m * f16_row_stride(k) * 2) + (size_t)m * sizeof(int);
+}
+
+int* f16_copy_exps(void* copy, int m, int k) {
+  return (int*)((uint8_t*)copy + align256((size_t)m * f16_row_stride(k) * 2));
+}
 
 void set_gemm_split(int split) { g_split_override = split; }
 
@@ -670,13 +688,10 @@ size_t gemm_workspace_bytes(int m, int n, int k) {
   return align256(f16_copy_bytes(m, k)) + (sp > 1 ? (size_t)sp * m * n * 4 : 0);
 }
 
-hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,
+hipError_t launch_x_to_f16(const float* x, _Float16* xh, int* rexp, int m, int k,
                            hipStream_t stream) {
-  const int kp = f16_row_stride(k);
-  const size_t items = (size_t)m * (kp / 8);
-  x_to_f16_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(x, xh, m,
-                                                                        k, kp);
-  return hipGetLastError();
+  RowCopyArgs a{x, xh, rexp, m, k, f16_row_stride(k), 0};
+  return launch_row_copy<kCopyRowMajor>(a, m, stream);
 }
 
 size_t gemm_partial_bytes(int m, int n, int k) {
@@ -684,9 +699,10 @@ size_t gemm_partial_bytes(int m, int n, int k) {
   return sp > 1 ? (size_t)sp * m * n * 4 : 0;
 }
 
-hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, float* y, int m,
-                           void* ws, size_t ws_bytes, hipStream_t stream,
+hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, const int* rexp, float* y,
+                           int m, void* ws, size_t ws_bytes, hipStream_t stream,
                            const Epilogue& epi, const GemmOut& out) {
+  if (rexp == nullptr) return hipErrorInvalidValue;
   const Geometry geo = geometry(w.n, w.k);
   GemmArgs a;
   a.qs = (const uint8_t*)w.base + w.qs_off;
@@ -694,6 +710,7 @@ hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, float* y, in
   a.mn = w.type == MLQ_Q4_1 ? (const uint8_t*)w.base + w.m_off : nullptr;
   a.x = nullptr;
   a.xh = xh;
+  a.rexp = rexp;
   a.y = y;
   a.m = m;
   a.n = w.n;
@@ -735,6 +752,7 @@ hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
   a.mn = w.type == MLQ_Q4_1 ? (const uint8_t*)w.base + w.m_off : nullptr;
   a.x = x;
   a.xh = nullptr;
+  a.rexp = nullptr;
   a.y = y;
   a.m = m;
   a.n = w.n;
@@ -754,9 +772,11 @@ hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
   if ((size_t)kBM * (size_t)w.k * 4 >= (1ull << 31)) return hipErrorInvalidValue;
   int xm = (w.k & 3) == 0 ? kXF32Vec : kXF32Scalar;
   if (ws != nullptr && ws_bytes >= f16_copy_bytes(m, w.k)) {
-    // one pass over x: fp16 copy, row stride kp, zero tail
+    // one pass over x: fp16 copy, row stride kp, zero tail, row exponents
     a.xh = (_Float16*)ws;
-    const hipError_t e = launch_x_to_f16(x, (_Float16*)ws, m, w.k, stream);
+    a.rexp = f16_copy_exps(ws, m, w.k);
+    const hipError_t e = launch_x_to_f16(x, (_Float16*)ws, f16_copy_exps(ws, m, w.k), m, w.k,
+                                         stream);
     if (e != hipSuccess) return e;
     xm = kXF16;
     // split K when the workspace also holds the partial slices

@@ -39,11 +39,16 @@
 //    converts and FMAs per group) it held ~60 more registers at depth 6,
 //    which capped how many groups a wave keeps in flight.
 //  - K slices combine through LDS in slice order (deterministic).
-// Activations must be finite and |x| < 65504 (the fp16 range of the hi part).
+//  - Any finite fp32 activations: each wave stages its slice of each row as
+//    x * 2^e (e = 0 when the row's largest |x| in the slice lies in
+//    [2^-10, 2^15), else the power of two that puts it in [2^14, 2^15)), and
+//    scales the row's results by 2^-e before the slices combine (exact
+//    power-of-two steps).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "../mlq_layout.h"
 #include "device_common.h"
@@ -172,10 +177,15 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi,
   lo = as_u32(l);
 }
 
-// hi/lo split of four activations written at column kl of rows 2r and 2r+1
-// of the wave's slice; returns their fp32 sum (q4_1 block sums).
+// hi/lo split of four activations, scaled by 2^e, written at column kl of
+// rows 2r and 2r+1 of the wave's slice; returns their scaled fp32 sum (q4_1
+// block sums).
 __device__ __forceinline__ float stage4(_Float16* xs, int xstride, int r,
-                                        int kl, float4 v) {
+                                        int kl, float4 v, int e) {
+  v.x = ldexp_f(v.x, e);
+  v.y = ldexp_f(v.y, e);
+  v.z = ldexp_f(v.z, e);
+  v.w = ldexp_f(v.w, e);
   uint2 hi, lo;
   split2(v.x, v.y, hi.x, lo.x);
   split2(v.z, v.w, hi.y, lo.y);
@@ -192,7 +202,10 @@ __device__ __forceinline__ float block_sum8(float v) {
   return v;
 }
 
-template <int QT, int MR, int GW, bool RING, bool NORM>
+// VEC: k % 4 == 0 (activation rows in whole float4). A compile-time choice:
+// a runtime branch around the activation loads makes the compiler wait for
+// all of them before the weight loads are issued.
+template <int QT, int MR, int GW, bool RING, bool NORM, bool VEC>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int M = a.m;
@@ -233,7 +246,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const int kbase = g0 * kGroupK;
   const int c4 = npad * (kGroupK / 4);
   const uint32_t xbytes = (uint32_t)min(ng * kGroupK, a.k - kbase) * 4u;
-  const bool vec = (a.k & 3) == 0;
+  constexpr bool vec = VEC;
   // Register-held part: MR == 1 covers 4 float4 per lane (8 groups); MR > 1
   // covers one float4 per lane of every row (2 groups). The rest, if any,
   // is staged after the weight loads are issued.
@@ -274,49 +287,150 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  // ---- per-row scale of the slice ------------------------------------------
+  // Every activation row of the slice is staged as x * 2^e, so any finite
+  // fp32 row fits the fp16 hi/lo pair: e = 0 while the row's largest |x| in
+  // the slice lies in [2^-10, 2^15), else e from that maximum
+  // (pow2_scale_exp). The row's results are scaled back by 2^-e before the
+  // slices combine. Values beyond the register-held part are read once more
+  // for this maximum.
+  constexpr int NR = MR == 1 ? 1 : kGemvMaxRows;
+  // Slices longer than the register-held part (MR == 1: > 8 groups; MR > 1:
+  // > 2 groups) read the rest once for the maximum and once to stage it.
+  const int c_done = MR == 1 ? 64 * XR : 64;
+  if constexpr (norm) {
+#pragma unroll
+    for (int i = 0; i < XR; ++i)
+      if (64 * i < c4) xr[i] = normed(xr[i], gr[i]);  // wave-uniform
+  }
+  // this lane's largest |x| of row r in the register-held part
+  auto reg_max = [&](int r) __attribute__((always_inline)) {
+    float mx = 0.0f;
+    if constexpr (MR == 1) {
+#pragma unroll
+      for (int i = 0; i < XR; ++i)
+        if (64 * i < c4 && lane + 64 * i < c4) mx = abs_max4(mx, xr[i]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < NR; ++q)
+        if (q == r && lane < c4) mx = abs_max4(mx, xr[q]);
+    }
+    return mx;
+  };
+  // ... and in the rest of a long slice (read once more)
+  auto rest_max = [&](int r) __attribute__((always_inline)) {
+    float mx = 0.0f;
+    const rsrc_t rx = make_rsrc(a.x + (size_t)r * a.k + kbase, xbytes);
+    for (int cb = c_done; cb < c4; cb += 64) {
+      float4 v = load_x4(rx, cb + lane, vec);
+      if constexpr (norm) {
+        const float4 g = load_x4(rg, cb + lane, vec);
+        v = float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
+      }
+      mx = abs_max4(mx, v);
+    }
+    return mx;
+  };
   // ---- stage hi/lo activations (+ q4_1 block sums) -----------------------
   // block sum of row r, block blk (of the slice) -> hi/lo halves at rows
-  // 2r, 2r+1 of group blk/4's A operand
+  // 2r, 2r+1 of group blk/4's A operand, stored as sum * 2^-6 (a block of
+  // 32 scaled values sums to at most 2^20; the MFMA result is scaled back by
+  // 64, exactly)
   auto stage_sum = [&](int r, int blk, float sx) {
+    sx = ldexp_f(sx, -6);
     const _Float16 hi = (_Float16)sx;
     const _Float16 lo = (_Float16)(sx - (float)hi);
     _Float16* g = xsa + (size_t)(blk >> 2) * kTileRows * kGroupBlocks + (blk & 3);
     g[(2 * r) * kGroupBlocks] = hi;
     g[(2 * r + 1) * kGroupBlocks] = lo;
   };
+  // Stages the slice, every row r scaled by 2^ex[r] (SCALED) or by 1. The
+  // unscaled pass also folds the input RMSNorm's sum of squares (once).
+  int ex[NR];  // wave-uniform: scalar registers
 #pragma unroll
-  for (int i = 0; i < XR; ++i) {
-    const int r = MR == 1 ? 0 : i;
-    const int c = MR == 1 ? lane + 64 * i : lane;
-    if (r < M && (MR > 1 || 64 * i < c4)) {  // wave-uniform
-      float sx = 0.0f;
-      float4 v = xr[i];
-      if constexpr (norm) v = normed(v, gr[i]);
-      if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, v);
-      if (QT == MLQ_Q4_1) {
-        sx = block_sum8(sx);
-        if (c < c4 && (c & 7) == 0) stage_sum(r, c >> 3, sx);
-      }
-    }
-  }
-  // Slices longer than the register-held part (MR == 1: > 8 groups; MR > 1:
-  // > 2 groups): the remainder, after the weight loads are in flight.
-  const int c_done = MR == 1 ? 64 * XR : 64;
-  if (c4 > c_done) {
-    for (int r = 0; r < M; ++r) {
-      const rsrc_t rx = make_rsrc(a.x + (size_t)r * a.k + kbase, xbytes);
-      for (int cb = c_done; cb < c4; cb += 64) {
-        const int c = cb + lane;
+  for (int r = 0; r < NR; ++r) ex[r] = 0;
+  auto stage = [&](auto scaled_c) __attribute__((always_inline)) {
+    constexpr bool SCALED = decltype(scaled_c)::value;
+#pragma unroll
+    for (int i = 0; i < XR; ++i) {
+      const int r = MR == 1 ? 0 : i;
+      const int c = MR == 1 ? lane + 64 * i : lane;
+      if (r < M && (MR > 1 || 64 * i < c4)) {  // wave-uniform
         float sx = 0.0f;
-        float4 v = load_x4(rx, c, vec);
-        if constexpr (norm) v = normed(v, load_x4(rg, c, vec));
-        if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, v);
+        if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, xr[i], SCALED ? ex[MR == 1 ? 0 : i] : 0);
         if (QT == MLQ_Q4_1) {
           sx = block_sum8(sx);
           if (c < c4 && (c & 7) == 0) stage_sum(r, c >> 3, sx);
         }
       }
     }
+    // the rest of long slices, after the weight loads are in flight
+    if (c4 > c_done) {
+      // (rows unrolled: a runtime row index into ex[] would put it in
+      // scratch memory)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        if (r >= M) break;  // wave-uniform
+        const rsrc_t rx = make_rsrc(a.x + (size_t)r * a.k + kbase, xbytes);
+        const int er = ex[r];
+        for (int cb = c_done; cb < c4; cb += 64) {
+          const int c = cb + lane;
+          float sx = 0.0f;
+          float4 v = load_x4(rx, c, vec);
+          if constexpr (norm) {
+            if constexpr (SCALED) {
+              const float4 g = load_x4(rg, c, vec);
+              v = float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
+            } else {
+              v = normed(v, load_x4(rg, c, vec));
+            }
+          }
+          if (c < c4) sx = stage4(xs, a.xstride, r, 4 * c, v, SCALED ? er : 0);
+          if (QT == MLQ_Q4_1) {
+            sx = block_sum8(sx);
+            if (c < c4 && (c & 7) == 0) stage_sum(r, c >> 3, sx);
+          }
+        }
+      }
+    }
+  };
+  // Rows whose largest |x| lies in [2^-10, 2^15) (the common case) keep
+  // scale 1: hi stays finite and the lo part's fp16 subnormal floor (2^-25)
+  // is below 2^-15 of the row's largest element, far inside the stated
+  // tolerance. The slice is staged with scale 1 right away while a
+  // wave-wide vote checks the window; only when a row falls outside it do
+  // the rows pay for their exact maxima (a cross-lane reduction) and a
+  // second, scaled staging pass.
+  stage(std::false_type{});
+  // Per lane: bit r = row r has a value >= 2^-10 here, bit 31 = some row
+  // has a value >= 2^15 here; one OR across the wave (VALU and a few scalar
+  // instructions: the scalar unit is shared by the CU's waves).
+  uint32_t flags = 0;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (r >= M) break;  // wave-uniform
+    const float mx = reg_max(r);
+    flags |= (mx >= 0x1p-10f ? 1u << r : 0u) | (mx >= 0x1p15f ? 1u << 31 : 0u);
+  }
+  if (c4 > c_done) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (r >= M) break;  // wave-uniform
+      const float mx = rest_max(r);
+      flags |= (mx >= 0x1p-10f ? 1u << r : 0u) | (mx >= 0x1p15f ? 1u << 31 : 0u);
+    }
+  }
+  const uint32_t all = wave_or(flags);
+  const bool unit = all == ((1u << M) - 1u);
+  if (!unit) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (r >= M) break;  // wave-uniform
+      float mx = reg_max(r);
+      if (c4 > c_done) mx = fmaxf(mx, rest_max(r));
+      ex[r] = __builtin_amdgcn_readfirstlane(pow2_scale_exp(wave_max_nonneg(mx)));
+    }
+    stage(std::true_type{});
   }
   // the slice is private to this wave: only LDS completion is needed
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
@@ -375,8 +489,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       if (MR > 1) acc1 = fmaf(df, D[b][2] + D[b][3], acc1);
     }
     if (QT == MLQ_Q4_1) {
-      acc0 += Dm[0] + Dm[1];
-      if (MR > 1) acc1 += Dm[2] + Dm[3];
+      acc0 += 64.0f * (Dm[0] + Dm[1]);
+      if (MR > 1) acc1 += 64.0f * (Dm[2] + Dm[3]);
     }
   };
 
@@ -400,6 +514,17 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   }
 
   // ---- output ------------------------------------------------------------
+  // undo the slice's power-of-two scale of activation rows r0 and r1
+  if (!unit) {
+    int e0 = ex[0], e1 = ex[0];
+#pragma unroll
+    for (int q = 1; q < NR; ++q) {
+      if (q == r0) e0 = ex[q];
+      if (q == r1) e1 = ex[q];
+    }
+    acc0 = ldexp_f(acc0, -e0);
+    if (MR > 1) acc1 = ldexp_f(acc1, -e1);
+  }
   // RMSNorm scale of the (single) row: sum(x^2) over lanes, then over the
   // K slices of the workgroup in slice order
   float nscale = 1.0f;
@@ -497,6 +622,8 @@ constexpr int kMaxDepth = 8;
 constexpr int kMaxDepthOneRow = 10;
 int max_depth(int type, int m) {
   if (type == MLQ_Q4_1) return m == 1 ? 7 : 3;
+  // q8_0 lines are twice as long: one group less than q4_0 fits
+  if (type == MLQ_Q8_0) return m == 1 ? kMaxDepthOneRow - 1 : kMaxDepth - 1;
   return m == 1 ? kMaxDepthOneRow : kMaxDepth;
 }
 // Ring depths that compile without spills, per type and row class.
@@ -575,19 +702,25 @@ Plan make_plan(int type, int m, const Geometry& geo) {
   return p;
 }
 
-template <int QT, int MR, int GW, bool RING, bool NORM>
-hipError_t launch_kernel(const GemvArgs& a, size_t lds, hipStream_t stream) {
+template <int QT, int MR, int GW, bool RING, bool NORM, bool VEC>
+hipError_t launch_vec(const GemvArgs& a, size_t lds, hipStream_t stream) {
   // Opt in to more than the default 64 KiB of dynamic LDS when needed.
   static size_t configured = 64 * 1024;
   if (lds > configured) {
     hipError_t e = hipFuncSetAttribute(
-        (const void*)gemv_kernel<QT, MR, GW, RING, NORM>,
+        (const void*)gemv_kernel<QT, MR, GW, RING, NORM, VEC>,
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     configured = lds;
   }
-  gemv_kernel<QT, MR, GW, RING, NORM><<<a.nt, 64 * a.split, lds, stream>>>(a);
+  gemv_kernel<QT, MR, GW, RING, NORM, VEC><<<a.nt, 64 * a.split, lds, stream>>>(a);
   return hipGetLastError();
+}
+
+template <int QT, int MR, int GW, bool RING, bool NORM>
+hipError_t launch_kernel(const GemvArgs& a, size_t lds, hipStream_t stream) {
+  if ((a.k & 3) == 0) return launch_vec<QT, MR, GW, RING, NORM, true>(a, lds, stream);
+  return launch_vec<QT, MR, GW, RING, NORM, false>(a, lds, stream);
 }
 
 // The input-RMSNorm variant exists for one activation row, and not for the
@@ -634,14 +767,19 @@ hipError_t launch_depth(const GemvArgs& a, const Plan& p, hipStream_t stream) {
     case 5: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 5, false>(a, p.lds, stream);
     case 6: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 6, false>(a, p.lds, stream);
     case 7: return launch_typed<QT, MR, (QT == MLQ_Q4_1 && MR > 1) ? 3 : 7, false>(a, p.lds, stream);
-    case 8: return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 7) : 8, false>(a, p.lds, stream);
+    case 8:
+      return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 7)
+                                  : (QT == MLQ_Q8_0 && MR > 1) ? 7 : 8, false>(a, p.lds, stream);
     default:
-      // 9 and 10: one activation row, q8_0 / q4_0 only
-      if constexpr (QT != MLQ_Q4_1 && MR == 1) {
+      // 9 and 10: one activation row, q8_0 (9) / q4_0 (10) only
+      if constexpr (QT == MLQ_Q8_0 && MR == 1) {
+        return launch_typed<QT, MR, 9, false>(a, p.lds, stream);
+      } else if constexpr (QT == MLQ_Q4_0 && MR == 1) {
         if (p.depth == 9) return launch_typed<QT, MR, 9, false>(a, p.lds, stream);
         return launch_typed<QT, MR, 10, false>(a, p.lds, stream);
       }
-      return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 7) : 8, false>(a, p.lds, stream);
+      return launch_typed<QT, MR, QT == MLQ_Q4_1 ? (MR > 1 ? 3 : 7)
+                                  : (QT == MLQ_Q8_0 && MR > 1) ? 7 : 8, false>(a, p.lds, stream);
   }
 }
 

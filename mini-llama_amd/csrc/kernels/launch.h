@@ -29,18 +29,14 @@ struct Epilogue {
   float norm_eps = 0.0f;
 };
 
-// Output options of the prefill GEMM reading the fp16 copy of x and of its
+// Output option of the prefill GEMM reading the fp16 copy of x and of its
 // split-K reduce (launch_gemm_f16, launch_gemm_ws with a workspace that
 // holds the copy; else hipErrorInvalidValue): residual [m][ny] added to the
 // output after the activation (may alias y: each element is read, then
-// written, by one thread), and with yh non-null the output is stored as
-// fp16 (round to nearest even, the rounding of launch_x_to_f16) at
-// yh[r * yh_ld + c] instead of y. Kept out of Epilogue so that the other
-// kernels' arguments do not grow.
+// written, by one thread). Kept out of Epilogue so that the other kernels'
+// arguments do not grow.
 struct GemmOut {
   const float* residual = nullptr;
-  _Float16* yh = nullptr;
-  int yh_ld = 0;
 };
 
 // capi.cpp: MLQ status of a HIP result, recorded for mlq_last_hip_error.
@@ -72,27 +68,37 @@ void set_gemv_split(int split);
 // splits K over gemm_splits(m, n, k) workgroups per output tile when
 // ws_bytes >= gemm_workspace_bytes(m, n, k) (fp32 partial slices after the
 // fp16 copy, summed in order by a second kernel).
+//
+// fp16 copies of activations carry one power-of-two exponent per row: row r
+// holds x[r] * 2^rexp[r] with rexp[r] = pow2_scale_exp(max |x[r]|), so any
+// finite fp32 row fits fp16 without overflow and far above its subnormal
+// floor; the GEMMs scale row r's fp32 results by 2^-rexp[r]. Without a copy
+// the GEMM finds the exponents of its rows itself before its K loop.
 hipError_t launch_gemm(const mlq_weight& w, const float* x, float* y, int m,
                        hipStream_t stream);
 hipError_t launch_gemm_ws(const mlq_weight& w, const float* x, float* y, int m,
                           void* ws, size_t ws_bytes, hipStream_t stream,
                           const Epilogue& epi = Epilogue(), const GemmOut& out = GemmOut());
+// Bytes of the fp16 copy of x [m][f16_row_stride(k)] plus its row exponents
+// (int32 [m] at f16_copy_exps).
 size_t f16_copy_bytes(int m, int k);
+int* f16_copy_exps(void* copy, int m, int k);
 // The GEMM from an fp16 copy of x already in place (xh [m][f16_row_stride(k)],
-// zero past k, e.g. written by launch_rmsnorm_f16 or a yh epilogue); `ws`
-// (gemm_partial_bytes(m, n, k), may be null when that is 0) takes the
-// split-K partial slices.
-hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, float* y, int m,
-                           void* ws, size_t ws_bytes, hipStream_t stream,
+// zero past k, with its row exponents rexp [m], e.g. written by
+// launch_rmsnorm_f16 or launch_x_to_f16); `ws` (gemm_partial_bytes(m, n, k),
+// may be null when that is 0) takes the split-K partial slices.
+hipError_t launch_gemm_f16(const mlq_weight& w, const _Float16* xh, const int* rexp, float* y,
+                           int m, void* ws, size_t ws_bytes, hipStream_t stream,
                            const Epilogue& epi = Epilogue(), const GemmOut& out = GemmOut());
 size_t gemm_partial_bytes(int m, int n, int k);
 int gemm_splits(int m, int n, int k);
 size_t gemm_workspace_bytes(int m, int n, int k);
 // Split-K override (0 = planner); validated by the caller.
 void set_gemm_split(int split);
-// fp16 copy of x [m][k] into xh [m][f16_row_stride(k)] (zero past k).
+// fp16 copy of x [m][k] into xh [m][f16_row_stride(k)] (zero past k), each
+// row scaled by 2^rexp[r] (the exponents written to rexp [m]).
 int f16_row_stride(int k);
-hipError_t launch_x_to_f16(const float* x, _Float16* xh, int m, int k,
+hipError_t launch_x_to_f16(const float* x, _Float16* xh, int* rexp, int m, int k,
                            hipStream_t stream);
 
 // Compute units of the current device (256 on MI355X), read once.
@@ -127,9 +133,11 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, int rows, in
                           float eps, hipStream_t stream);
 // RMSNorm rows written as fp16 (round to nearest even) into yh [rows][ld],
 // zero for dim <= c < ld: the GEMM's fp16 copy of its input in one pass.
-// Needs dim % 4 == 0, ld % 4 == 0 and 16-byte aligned x, w, yh rows.
-hipError_t launch_rmsnorm_f16(const float* x, const float* w, _Float16* yh, int rows, int dim,
-                              int ld, float eps, hipStream_t stream);
+// Row r is stored scaled by 2^rexp[r] (pow2_scale_exp of the row's largest
+// |y|), the convention of launch_x_to_f16. Needs dim % 4 == 0, ld % 4 == 0
+// and 16-byte aligned x, w, yh rows.
+hipError_t launch_rmsnorm_f16(const float* x, const float* w, _Float16* yh, int* rexp, int rows,
+                              int dim, int ld, float eps, hipStream_t stream);
 // bytes (a multiple of 4) of zeros at p (4-byte aligned): a kernel, so it
 // may be captured in a graph.
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
@@ -199,9 +207,6 @@ struct AttnLaunch {
   // pos + r, q row r at q + r * q_stride, output row at out + r * out_stride;
   // ws holds attention_workspace_bytes(n_heads, hd, max_len, rows).
   int rows = 1, q_stride = 0, out_stride = 0;
-  // launch_attention_prefill only: fp16 output rows (round to nearest
-  // even) at out_h + r * out_stride instead of out
-  _Float16* out_h = nullptr;
 };
 bool attention_supported(int n_heads, int n_kv, int hd);
 bool attention_fusable(int hd, int group);

@@ -7,8 +7,10 @@
 // grid (workgroups over 16-row weight tiles, their waves splitting K, so the
 // weights stream from HBM once with 256+ workgroups in flight) and runs the
 // rows of x through v_mfma_f32_16x16x32_f16 in blocks of 16:
-//  - x comes from an fp16 copy that mlq_linear_ws makes first, written in
-//    MFMA fragment order (rows padded to 16; per 128-k group, row block and
+//  - x comes from an fp16 copy that mlq_linear_ws makes first (each row
+//    scaled by a power of two from its largest |x|, undone on the fp32
+//    results, so any finite fp32 row fits fp16), written in MFMA fragment
+//    order (rows padded to 16; per 128-k group, row block and
 //    32-k block one run of 64 lanes x 16 bytes), so every x fragment load
 //    of a wave is 1 KiB contiguous (L2-resident). x is re-read by every
 //    workgroup: its load volume, not the weight stream, bounds the kernel
@@ -40,6 +42,7 @@
 #include "../mlq_layout.h"
 #include "device_common.h"
 #include "launch.h"
+#include "row_copy.h"
 
 namespace mlq {
 namespace {
@@ -52,6 +55,7 @@ struct SkinnyArgs {
   const uint8_t* d;
   const uint8_t* mn;
   const _Float16* xf;  // fragment-ordered fp16 copy of x (skinny_x_bytes)
+  const int* rexp;     // row exponents of the copy: row r holds x[r] * 2^rexp[r]
   float* y;
   int m, n, g, nt;
   Epilogue epi;
@@ -203,9 +207,20 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyArgs a) {
   if (j < ng) run(gr[0], gr[1], j);
 
   // lane holds D[4*(lane/16) + i][lane%16]: activation row 16mb + 4(lane/16)
-  // + i, weight row lane%16 of tile t. K slices combine in slice order, one
-  // tile at a time.
+  // + i, weight row lane%16 of tile t. Each row is scaled back by 2^-e of
+  // its exponent; K slices combine in slice order, one tile at a time.
   const int col = lane & 15, rq4 = 4 * (lane >> 4);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int4 e4 = *(const int4*)(a.rexp + 16 * mb + rq4);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      acc[t][mb][0] = ldexp_f(acc[t][mb][0], -e4.x);
+      acc[t][mb][1] = ldexp_f(acc[t][mb][1], -e4.y);
+      acc[t][mb][2] = ldexp_f(acc[t][mb][2], -e4.z);
+      acc[t][mb][3] = ldexp_f(acc[t][mb][3], -e4.w);
+    }
+  }
   const bool split = a.splits > 1;
   // outputs of tile t from `sum` (K slices of the workgroup): the epilogue
   // into y
@@ -254,37 +269,6 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(SkinnyArgs a) {
     }
     if (t + 1 < T) __syncthreads();
   }
-}
-
-// x fp32 [m][k] -> the fragment-ordered fp16 copy: element (r, c) of row
-// block mb = r/16, 128-k group j = c/128, 32-k block b = c%128/32 sits at
-// lane r%16 + 16*(c%32/8), position c%8 of run ((j*mbt + mb)*4 + b);
-// rows >= m and columns >= k are zero. One thread per 16-byte chunk.
-__global__ __launch_bounds__(256) void x_to_frag_kernel(const float* x, _Float16* xf,
-                                                        int m, int k, int kp, int mbt) {
-  const int per_row = kp / 8;
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (size_t)mbt * 16 * per_row) return;
-  const int r = (int)(idx / per_row), c0 = (int)(idx % per_row) * 8;
-  float v[8];
-  const float* xr = x + (size_t)r * k;
-  if (r < m && (k & 3) == 0 && c0 + 8 <= k) {
-    const float4 lo = *(const float4*)(xr + c0);
-    const float4 hi = *(const float4*)(xr + c0 + 4);
-    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (r < m && c0 + e < k) ? xr[c0 + e] : 0.0f;
-  }
-  uint4 o;
-  o.x = pack_h2(v[0], v[1]);
-  o.y = pack_h2(v[2], v[3]);
-  o.z = pack_h2(v[4], v[5]);
-  o.w = pack_h2(v[6], v[7]);
-  const int j = c0 / kGroupK, b = (c0 % kGroupK) / 32, kq = (c0 % 32) / 8;
-  const int mb = r / 16, lane = r % 16 + 16 * kq;
-  *(uint4*)(xf + ((((size_t)j * mbt + mb) * 4 + b) * 64 + lane) * 8) = o;
 }
 
 int g_tiles_override = 0;   // mlq_set_skinny_plan; 0 = planner
@@ -372,10 +356,16 @@ void set_skinny_plan(int tiles, int splits) {
   g_splits_override = splits;
 }
 
-// x copy, then (split K) the partial slices.
+// x copy, its row exponents (one per padded row), then (split K) the
+// partial slices.
+size_t skinny_exp_offset(int m, int k) { return align256(skinny_x_bytes(m, k)); }
+size_t skinny_part_offset(int m, int k) {
+  return skinny_exp_offset(m, k) + align256((size_t)(m + 15) / 16 * 16 * sizeof(int));
+}
+
 size_t skinny_workspace_bytes(int type, int m, int n, int k) {
   const SkinnyPlan p = skinny_plan(type, m, n, k);
-  size_t b = align256(skinny_x_bytes(m, k));
+  size_t b = skinny_part_offset(m, k);
   if (p.splits > 1) b += (size_t)p.splits * m * n * 4;
   return b;
 }
@@ -395,6 +385,8 @@ hipError_t launch_skinny_ws(const mlq_weight& w, const float* x, float* y, int m
   a.d = (const uint8_t*)w.base + w.d_off;
   a.mn = w.type == MLQ_Q4_1 ? (const uint8_t*)w.base + w.m_off : nullptr;
   a.xf = (const _Float16*)ws;
+  int* rexp = (int*)((uint8_t*)ws + skinny_exp_offset(m, w.k));
+  a.rexp = rexp;
   a.y = y;
   a.m = m;
   a.n = w.n;
@@ -403,16 +395,12 @@ hipError_t launch_skinny_ws(const mlq_weight& w, const float* x, float* y, int m
   a.epi = epi;
   a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
   a.splits = p.splits;
-  a.part = p.splits > 1
-      ? (float*)((uint8_t*)ws + align256(skinny_x_bytes(m, w.k)))
-      : nullptr;
+  a.part = p.splits > 1 ? (float*)((uint8_t*)ws + skinny_part_offset(m, w.k)) : nullptr;
   // fragment-ordered fp16 copy of x
   const int kp = (w.k + kGroupK - 1) / kGroupK * kGroupK;
   const int mbt = (m + 15) / 16;
-  const size_t items = (size_t)mbt * 16 * (kp / 8);
-  x_to_frag_kernel<<<(unsigned)((items + 255) / 256), 256, 0, stream>>>(
-      x, (_Float16*)ws, m, w.k, kp, mbt);
-  hipError_t e = hipGetLastError();
+  const RowCopyArgs ca{x, (_Float16*)ws, rexp, m, w.k, kp, mbt};
+  hipError_t e = launch_row_copy<kCopyFragments>(ca, mbt * 16, stream);
   if (e != hipSuccess) return e;
   switch (w.type) {
     case MLQ_Q8_0: e = launch_typed<MLQ_Q8_0>(a, p.tiles, stream); break;

@@ -61,7 +61,8 @@ def tolerance_ok(y, ref, x2d, k):
     y = np.atleast_2d(y)
     ref = np.atleast_2d(ref)
     x2d = np.atleast_2d(x2d)
-    atol = 1e-3 * np.linalg.norm(x2d, axis=1, keepdims=True) * np.sqrt(k / 4096)
+    # (the norm in float64: rows near the fp32 limit must not make it inf)
+    atol = 1e-3 * np.linalg.norm(x2d.astype(np.float64), axis=1, keepdims=True) * np.sqrt(k / 4096)
     err = np.abs(y.astype(np.float64) - ref.astype(np.float64))
     return (err <= atol) | (err <= 2e-3 * np.abs(ref))
 
@@ -70,7 +71,7 @@ def error_report(y, ref, x2d, k):
     y = np.atleast_2d(y).astype(np.float64)
     ref = np.atleast_2d(ref).astype(np.float64)
     x2d = np.atleast_2d(x2d)
-    atol = 1e-3 * np.linalg.norm(x2d, axis=1, keepdims=True) * np.sqrt(k / 4096)
+    atol = 1e-3 * np.linalg.norm(x2d.astype(np.float64), axis=1, keepdims=True) * np.sqrt(k / 4096)
     err = np.abs(y - ref)
     rel = err / np.maximum(np.abs(ref), 1e-30)
     return {"max_abs_over_atol": float((err / atol).max()),
