@@ -267,12 +267,14 @@ def argmax(x) -> int:
     return int(_fwd().ref_argmax(_ptr(x), x.size))
 
 
-def linear_weight(x, w: dict) -> np.ndarray:
+def linear_weight(x, w: dict, threads: int = 1) -> np.ndarray:
     """The Linear dispatch of forwardLinear's CPU branch (ops.cc:28-40) for a
-    model-dict weight {"type", "shape", "data"}."""
+    model-dict weight {"type", "shape", "data"}. `threads` splits the output
+    rows like the reference ThreadPool (each output is one thread's
+    sequential sum, so the result does not depend on it)."""
     if w["type"] == "f32":
         return linear_f32(x, np.asarray(w["data"], np.float32).reshape(w["shape"]))
-    return linear(_f32(x).reshape(-1), w["data"], w["shape"], w["type"])
+    return linear(_f32(x).reshape(-1), w["data"], w["shape"], w["type"], threads=threads)
 
 
 def new_cache(model: dict):
@@ -283,10 +285,11 @@ def new_cache(model: dict):
     return np.zeros(shape, np.float32), np.zeros(shape, np.float32)
 
 
-def forward_token(model: dict, cache, token: int, pos: int) -> np.ndarray:
+def forward_token(model: dict, cache, token: int, pos: int, threads: int = 1) -> np.ndarray:
     """forwardToken's CPU branch (forward.cc:763-797): embedding, every
     forwardLayer (:642-730) and computelogits (:747-761). `cache` is the
-    (keys, values) pair from new_cache, updated at `pos` in place."""
+    (keys, values) pair from new_cache, updated at `pos` in place.
+    `threads`: the quantized Linears' thread count (same results)."""
     c = model["config"]
     keys, values = cache
     nh, nkv = c["n_heads"], c["n_kv_heads"]
@@ -299,7 +302,7 @@ def forward_token(model: dict, cache, token: int, pos: int) -> np.ndarray:
         h = rmsnorm(x, lw["attention_norm"], eps)
         parts = []
         for wname, bname in (("wq", "bq"), ("wk", "bk"), ("wv", "bv")):
-            y = linear_weight(h, lw[wname])
+            y = linear_weight(h, lw[wname], threads)
             b = lw.get(bname)
             if b is not None and np.size(b):
                 y = (y + _f32(b)).astype(np.float32)  # addOptionalBias (:402-416)
@@ -309,10 +312,10 @@ def forward_token(model: dict, cache, token: int, pos: int) -> np.ndarray:
         keys[li, pos] = k
         values[li, pos] = parts[2].reshape(nkv, hd)
         att = attention(q, keys, values, li, pos)
-        proj = linear_weight(att.reshape(-1), lw["wo"])
+        proj = linear_weight(att.reshape(-1), lw["wo"], threads)
         x = (x + proj).astype(np.float32)  # forwardAdd (:312-330)
         h = rmsnorm(x, lw["ffn_norm"], eps)
-        ff = linear_weight(swiglu(linear_weight(h, lw["w_gate"]), linear_weight(h, lw["w_up"])),
-                           lw["w_down"])
+        ff = linear_weight(swiglu(linear_weight(h, lw["w_gate"], threads),
+                                  linear_weight(h, lw["w_up"], threads)), lw["w_down"], threads)
         x = (x + ff).astype(np.float32)
-    return linear_weight(rmsnorm(x, model["final_norm"], eps), model["lm_head"])
+    return linear_weight(rmsnorm(x, model["final_norm"], eps), model["lm_head"], threads)

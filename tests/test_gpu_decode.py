@@ -595,6 +595,17 @@ PREFILL_CASES = [
     # and q4_1 fused with biases through the prefill GEMM
     ("f32", {"cfg": {"dim": 128, "n_heads": 4, "n_kv_heads": 2}, "bias": True}, True, 2, 70),
     ("q4_1", {"cfg": {"dim": 256, "n_heads": 8, "n_kv_heads": 2}, "bias": True}, True, 0, 129),
+    # 512-token prompts with GQA groups that are not powers of two (the MFMA
+    # prefill attention pads them to 4 / 8 heads, padding heads masked) at
+    # head_dim 64, 128 and 256
+    ("q4_0", {"cfg": {"dim": 384, "n_heads": 6, "n_kv_heads": 2, "max_seq_len": 600,
+                      "rope_type": 1}}, True, 0, 512),
+    ("q8_0", {"cfg": {"dim": 1280, "n_heads": 10, "n_kv_heads": 2, "max_seq_len": 600},
+              "bias": True}, True, 3, 512),
+    ("q4_0", {"cfg": {"dim": 1792, "n_heads": 7, "n_kv_heads": 1, "max_seq_len": 600,
+                      "rope_type": 1}}, True, 0, 512),
+    ("q4_1", {"cfg": {"dim": 896, "n_heads": 7, "n_kv_heads": 1, "max_seq_len": 600}}, True,
+     1, 512),
 ]
 
 
@@ -639,6 +650,42 @@ def test_prefill_matches_sequential_oracle(pkg, oracle, cuda, qtype, kw, fuse, s
         ref = oracle.forward_token(model, cache, tokens[p], p)
         got = dm.forward_token(tokens[p], p).cpu().numpy()
         assert np.abs(got - ref).max() <= rel * np.abs(ref).max() + 1e-6, p
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+def test_prefill_qwen2_7b_layer_at_full_size(pkg, oracle, cuda, qtype):
+    """One Qwen2-7B-shaped layer (dim 3584, FFN 18944, 28 heads / 4 kv
+    heads: GQA group 7, head_dim 128, q|k|v biases, NeoX RoPE) prefilled over
+    512 tokens, the benchmarked prefill workload, against the oracle run
+    token by token: last logits, every K/V row, and one decode step after.
+    q8_0 at this size takes the large-grid prefill GEMM variant (two
+    workgroups per CU)."""
+    import os
+    import mini_llama_amd.decode as dec
+    import mini_llama_amd.synth as synth
+    cfg = dict(vocab_size=256, dim=3584, hidden_dim=18944, n_layers=1, n_heads=28,
+               n_kv_heads=4, max_seq_len=520, rope_theta=1e6, rms_norm_eps=1e-6, rope_type=1)
+    model = synth.synthetic_model(cfg, qtype, seed=9, bias=True)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    n = 512
+    tokens = np.random.default_rng(4).integers(0, cfg["vocab_size"], n + 1).tolist()
+    print(f"prefill full-size {qtype}: oracle over {n} tokens ({threads} threads)", flush=True)
+    cache = oracle.new_cache(model)
+    for p in range(n):
+        ref = oracle.forward_token(model, cache, tokens[p], p, threads=threads)
+    dm = dec.DecodeModel(model)
+    got = dm.prefill(tokens[:n], 0).cpu().numpy()
+    scale = np.abs(ref).max()
+    err = np.abs(got - ref).max()
+    print(f"prefill full-size {qtype}: logits error / max = {err / scale:.2e}", flush=True)
+    assert err <= 2e-3 * scale + 1e-6
+    keys, values = dm.keys.cpu().numpy(), dm.values.cpu().numpy()
+    for arr, want in ((keys, cache[0]), (values, cache[1])):
+        amax = np.abs(want[:, :n]).max()
+        assert np.abs(arr[:, :n] - want[:, :n]).max() <= 2e-2 * amax + 2.4e-7 * n * amax
+    ref = oracle.forward_token(model, cache, tokens[n], n, threads=threads)
+    got = dm.forward_token(tokens[n], n).cpu().numpy()
+    assert np.abs(got - ref).max() <= 2e-3 * np.abs(ref).max() + 1e-6
 
 
 def test_prefill_tiny_model_greedy(pkg, oracle, cuda):
