@@ -10,22 +10,31 @@ The timed launches are captured in one HIP graph and bracketed by HIP events
 on the stream they run on.
 
 Also reported in the same line: the q8_0 prefill GEMM (configs[4], M=512,
-W [11008, 4096]) in TFLOP/s against the dense fp16 MFMA peak, and the
-reference CPU path (the oracle restatement) timed on the host cores.
-`configs` holds the other BASELINE configurations (configs[0], [2] and [3]
-at M = 4, 16, 64) in GB/s and fraction of 8 TB/s; `--all` adds the
-196-GEMV decode sweeps and the GGUF upload rate.
+W [11008, 4096]) in TFLOP/s against the dense fp16 MFMA peak; `configs`
+holds the other BASELINE configurations (configs[0], [2] and [3] at M = 4,
+16, 64 for q4_0, 16 and 64 for q8_0 / q4_1) in GB/s and fraction of 8 TB/s,
+and configs[4]'s 196-GEMV decode sweep (28 Qwen2-7B layers x q,k,v,o,gate,
+up,down at M = 1) launched separately, fused (q|k|v, gate|up) and fused
+with the bias / SwiGLU epilogues; `roofline.read_ceiling` is one plain
+streaming read of the headline's weight bytes (mlq_read_probe), the
+single-launch ceiling the headline is compared against.
 `decode_step` reports whole-model decode: a Qwen2-7B-shaped q4_0
 model stepped token by token through mlq_decode_token, captured with its
 greedy sampling as one HIP graph, in tokens/s and algorithmic GB/s (weights
-+ KV cache rows read per token).
++ KV cache rows read per token), and its 512-token prefill; `prefill_q8_0`
+is the same prefill on a q8_0 model. `cpu_baseline` is the reference CPU
+path (the oracle restatement) on the host cores, one thread per physical
+core up to the job's 16-thread CPU share, with lscpu's figures. `--all`
+adds the GGUF upload rate.
 
 Profiling modes (one kernel family per run, for rocprofv3 counter passes):
 `--mode headline` launches only the headline GEMV (eagerly with `--eager`),
 `--mode copy` runs a plain device-to-device copy of 256 MiB, the known-size
 reference that scales the FETCH_SIZE / WRITE_SIZE counters to bytes;
 `--mode case --case qtype,m,n,k` launches one Linear shape (the skinny and
-prefill GEMM counter summaries in profiles/ come from it).
+prefill GEMM counter summaries in profiles/ come from it), `--mode
+read-ceiling` times the read probe at every BASELINE weight size and
+`--mode sweep` the three 196-GEMV sweeps alone.
 `roofline.traffic` is read from profiles/hbm_traffic_gemv_q4_0_c1.md (the
 summary of those counter runs) when it is present, else null.
 """
@@ -168,44 +177,55 @@ SWEEP_SHAPES = [("q", 3584, 3584), ("k", 512, 3584), ("v", 512, 3584),
 def bench_sweep(pkg, torch, steps, warmup, mode):
     """28 layers x {q,k,v,o,gate,up,down} q4_0 GEMVs (hidden 3584, FFN 18944,
     GQA kv 512), M = 1, one fixed x per input size, one graph = one decode
-    step. mode "fused" uploads q|k|v and gate|up as concatenated weights
-    (each pair/triple shares its input), so a layer is 4 launches instead
-    of 7; "epilogue" also adds the q|k|v bias in the kernel (Qwen2 has one)
-    and interleaves gate|up for the SwiGLU epilogue, which writes
-    silu(gate) * up (18944 floats instead of 2 x 18944) — the decode step's
-    Linear work with no separate bias, SiLU or multiply launch. The weight
-    bytes and flops are the same in every mode."""
+    step's Linear work (3.67 GB of weights, far past the 256 MB Infinity
+    Cache). mode "separate" launches the 196 GEMVs one by one; "fused"
+    repacks q|k|v and gate|up as concatenated weights (each pair/triple
+    shares its input), so a layer is 4 launches instead of 7; "epilogue"
+    also adds the q|k|v bias in the kernel (Qwen2 has one) and interleaves
+    gate|up for the SwiGLU epilogue, which writes silu(gate) * up (18944
+    floats instead of 2 x 18944) — no separate bias, SiLU or multiply
+    launch. The weight bytes and flops are the same in every mode. Blocks are
+    generated on the device and repacked there (mlq_repack_device)."""
     import mini_llama_amd.synth as synth
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5000)
     xs = {kk: torch.from_numpy(synth.make_x(1, kk, 900 + kk)[0]).to("cuda")
           for kk in (3584, 18944)}
-    log(f"sweep ({mode}): uploading 28 layers")
+    bb = GGUF_BLOCK["q4_0"]
+    log(f"sweep ({mode}): building 28 layers on the device")
     calls = []
     for layer in range(28):
-        blk = {name: (synth.make_blocks("q4_0", n, k, 5000 + 10 * layer + i), n, k)
-               for i, (name, n, k) in enumerate(SWEEP_SHAPES)}
+        blk = {name: (synth.device_blocks(torch, gen, "q4_0", n, k, 1.0 / np.sqrt(k), "cuda"),
+                      n, k) for name, n, k in SWEEP_SHAPES}
         if mode == "separate":
             groups = [[name] for name, _, _ in SWEEP_SHAPES]
         else:
             groups = [["q", "k", "v"], ["o"], ["gate", "up"], ["down"]]
         for g in groups:
             k = blk[g[0]][2]
+            row = ((k + 31) // 32) * bb
             bias, act = None, pkg.EPI_NONE
             if len(g) == 1:
-                w = pkg.upload("q4_0", blk[g[0]][0], blk[g[0]][1], k, device="cuda")
+                aos, n = blk[g[0]][0], blk[g[0]][1]
             elif mode == "epilogue" and g[0] == "gate":
                 ffn = blk["gate"][1]
-                w = pkg.upload_glu("q4_0", blk["gate"][0], blk["up"][0], ffn, k,
-                                   device="cuda")
-                act = pkg.EPI_SWIGLU
+                # 16-row tiles of 8 gate rows then the matching 8 up rows
+                aos = torch.stack([blk["gate"][0].view(ffn // 8, 8 * row),
+                                   blk["up"][0].view(ffn // 8, 8 * row)], dim=1).reshape(-1)
+                n, act = 2 * ffn, pkg.EPI_SWIGLU
             else:
-                w, _ = pkg.upload_concat("q4_0", [(blk[nm][0], blk[nm][1]) for nm in g],
-                                         k, device="cuda")
+                aos = torch.cat([blk[nm][0] for nm in g])
+                n = sum(blk[nm][1] for nm in g)
                 if mode == "epilogue":
-                    bias = torch.from_numpy(synth.make_x(1, w.n, 77 + layer)[0]).to("cuda")
-            ny = w.n // 2 if act == pkg.EPI_SWIGLU else w.n
+                    bias = torch.from_numpy(synth.make_x(1, n, 77 + layer)[0]).to("cuda")
+            w = pkg.repack_device("q4_0", aos, n, k)
+            del aos
+            ny = n // 2 if act == pkg.EPI_SWIGLU else n
             y = torch.empty(ny, dtype=torch.float32, device="cuda")
             calls.append((w, xs[k], y, bias, act))
-    del blk
+        del blk
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
 
     def step(_):
         for w, x, y, bias, act in calls:
@@ -213,13 +233,59 @@ def bench_sweep(pkg, torch, steps, warmup, mode):
 
     steps = max(1, steps)
     sec = time_graph(torch, step, steps, warmup) / steps
+    for _, _, y, _, _ in calls:
+        assert torch.isfinite(y).all().item()
     total = sum(alg_bytes("q4_0", 1, n, k) for _ in range(28) for _, n, k in SWEEP_SHAPES)
     flops = sum(alg_flops(1, n, k) for _ in range(28) for _, n, k in SWEEP_SHAPES)
     launches = len(calls)
     del calls
     torch.cuda.empty_cache()
+    log(f"sweep ({mode}): {sec * 1e6:.1f} us/step, {total / sec / 1e9:.0f} GB/s")
     return {"gemvs": 196, "launches": launches, "us_per_step": sec * 1e6,
             "gbs": total / sec / 1e9, "bytes": total, "tflops": flops / sec / 1e12}
+
+
+READ_SIZES = [("c0 q8_0 4096x4096", "q8_0", 4096, 4096),
+              ("c1 q4_0 18944x3584", "q4_0", 18944, 3584),
+              ("c2 q4_1 4096x14336", "q4_1", 4096, 14336),
+              ("c3 q4_0 4096x4096", "q4_0", 4096, 4096),
+              ("c4 q8_0 11008x4096", "q8_0", 11008, 4096),
+              ("q|k|v q4_0 4608x3584", "q4_0", 4608, 3584),
+              ("gate|up q4_0 37888x3584", "q4_0", 37888, 3584)]
+
+
+def bench_read_ceiling(pkg, torch, steps, warmup, sizes=None):
+    """HBM read ceiling of ONE launch per size: mlq_read_probe (a streaming
+    dwordx4 read, nothing else) over the tiled bytes of each BASELINE
+    weight, plus 256 MiB and 1 GiB for the asymptote. Launches rotate over
+    distinct regions of a pool of >= 512 MB + size (no Infinity-Cache reuse)
+    and are timed as one HIP graph like the Linear cases."""
+    sizes = READ_SIZES if sizes is None else sizes
+    items = [(name, int(pkg.weight_layout(qt, n, k).bytes)) for name, qt, n, k in sizes]
+    items += [("256 MiB", 256 << 20), ("1 GiB", 1 << 30)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = {}
+    for name, nbytes in items:
+        nbytes = nbytes // 16 * 16
+        stride = -(-nbytes // 4096) * 4096
+        slots = max(2, -(-ROTATE_BYTES // stride) + 1)
+        pool = torch.empty(slots * stride, dtype=torch.uint8, device="cuda")
+        pool.fill_(0)  # first touch outside the timed region
+        views = [pool[i * stride:i * stride + nbytes] for i in range(slots)]
+
+        def launch(i):
+            pkg.read_probe(views[i % slots], nbytes, sink)
+        n_steps = max(10, min(steps, int(4e10 // nbytes)))
+        sec = time_graph(torch, launch, n_steps, warmup) / n_steps
+        out[name] = {"bytes": nbytes, "us": round(sec * 1e6, 3),
+                     "gbs": round(nbytes / sec / 1e9, 1),
+                     "frac_hbm": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+                     "copies": slots}
+        log(f"read ceiling {name}: {nbytes} B, {sec * 1e6:.2f} us, {nbytes / sec / 1e9:.0f} GB/s")
+        del views, pool
+        torch.cuda.empty_cache()
+    assert int(sink.item()) == 0
+    return out
 
 
 def bench_gguf_load(pkg, torch, layers=4):
@@ -368,7 +434,59 @@ def bench_prefill(dm, torch, n, reps):
             "linear_tflops": flops / (ms * 1e-3) / 1e12, "reps": reps}
 
 
-def cpu_baseline(qtype, n, k, budget_s=10.0, flavor="scalar"):
+def bench_prefill_model(pkg, torch, qtype, n, reps):
+    """mlq_prefill of an n-token prompt on a Qwen2-7B-shaped model of
+    another block type (the decode-step model is q4_0)."""
+    import mini_llama_amd.decode as dec
+    import mini_llama_amd.synth as synth
+    log(f"prefill: building a {QWEN2_7B['n_layers']}-layer {qtype} model on the device")
+    model = synth.synthetic_model_device(QWEN2_7B, qtype, seed=9, bias=True)
+    dm = dec.DecodeModel(model)
+    del model
+    out = bench_prefill(dm, torch, n, reps)
+    out["workload"] = (f"Qwen2-7B-shaped {qtype} prefill of {n} tokens at position 0 "
+                       "(every Linear on [n, K], attention, lm_head on the last row)")
+    del dm
+    return {kk: (round(v, 4) if isinstance(v, float) else v) for kk, v in out.items()}
+
+
+CPU_SHARE = 16  # host threads one GPU's job may use on the GPU boxes
+
+
+def host_cpu():
+    """lscpu's view of the host: model, sockets, physical cores, threads,
+    plus the CPUs this process may run on (its affinity mask)."""
+    info = {}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except Exception:  # lscpu absent: affinity only
+        pass
+
+    def num(key):
+        try:
+            return int(info.get(key, ""))
+        except ValueError:
+            return None
+    sockets, per_socket, per_core = num("Socket(s)"), num("Core(s) per socket"), num("Thread(s) per core")
+    physical = sockets * per_socket if sockets and per_socket else None
+    return {"model": info.get("Model name"), "sockets": sockets, "cores_per_socket": per_socket,
+            "threads_per_core": per_core, "physical_cores": physical,
+            "logical_cpus": num("CPU(s)"), "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def cpu_threads(cpu):
+    """Threads for the CPU leg: one per physical core the process may use
+    (the reference's default is hardware_concurrency, src/threadpool.cc:13-20),
+    capped at the job's CPU share on the GPU boxes."""
+    cores = cpu["physical_cores"] or cpu["affinity_cpus"]
+    return max(1, min(cores, cpu["affinity_cpus"], CPU_SHARE))
+
+
+def cpu_baseline(qtype, n, k, budget_s=10.0, flavor="scalar", threads=None):
     """The reference CPU path (oracle restatement of linearQ40 / linearQ80
     with the reference thread partition), timed on this host's cores; flavor
     "avx2" is the build with the reference's AVX2 q8_0 loop (quant.cc:505-628;
@@ -376,7 +494,8 @@ def cpu_baseline(qtype, n, k, budget_s=10.0, flavor="scalar"):
     oracle = graft.load_oracle()
     graft.load_package()
     import mini_llama_amd.synth as synth
-    threads = max(1, min(16, os.cpu_count() or 1))
+    if threads is None:
+        threads = cpu_threads(host_cpu())
     blocks = synth.make_blocks(qtype, n, k, 1)
     x = synth.make_x(1, k, 2)[0]
     oracle.linear(x, blocks, (n, k), qtype, threads=threads, flavor=flavor)  # warm
@@ -402,10 +521,11 @@ def main():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--all", action="store_true",
-                    help="also run the decode sweeps and the GGUF upload timing")
+                    help="also run the GGUF upload timing and the extra bench shapes")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--mode", choices=["full", "headline", "copy", "decode", "case"],
+    ap.add_argument("--mode", choices=["full", "headline", "copy", "decode", "case",
+                                       "read-ceiling", "sweep"],
                     default="full", help="headline/copy/decode/case: profiling runs")
     ap.add_argument("--case", default="q4_0,16,4096,4096",
                     help="--mode case: qtype,m,n,k of the one shape to launch")
@@ -437,6 +557,15 @@ def main():
     if args.mode == "decode":
         r = bench_decode(pkg, torch, min(args.steps, 200), args.warmup, args.context)
         print(json.dumps({"mode": "decode", **r}), flush=True)
+        return
+    if args.mode == "read-ceiling":
+        r = bench_read_ceiling(pkg, torch, args.steps, args.warmup)
+        print(json.dumps({"mode": "read-ceiling", "sizes": r}), flush=True)
+        return
+    if args.mode == "sweep":
+        r = {mode: bench_sweep(pkg, torch, max(1, args.steps // 100), 1, mode)
+             for mode in ("separate", "fused", "epilogue")}
+        print(json.dumps({"mode": "sweep", **r}), flush=True)
         return
     if args.mode == "case":
         qt, m, n, k = args.case.split(",")
@@ -489,33 +618,64 @@ def main():
     except Exception as e:  # reported, never fatal to the headline line
         result["decode_step"] = {"error": f"{type(e).__name__}: {e}"}
     torch.cuda.empty_cache()
+    try:
+        result["prefill_q8_0"] = bench_prefill_model(pkg, torch, "q8_0", 512,
+                                                     max(2, min(args.steps, 200) // 25))
+    except Exception as e:  # reported, never fatal to the headline line
+        result["prefill_q8_0"] = {"error": f"{type(e).__name__}: {e}"}
+    torch.cuda.empty_cache()
     # every other BASELINE config (GEMV / skinny shapes), a few seconds each
     extra = {}
     for name, qt, m, n, k in [("c0", "q8_0", 1, 4096, 4096),
                               ("c2", "q4_1", 1, 4096, 14336),
                               ("c3_m4", "q4_0", 4, 4096, 4096),
                               ("c3_m16", "q4_0", 16, 4096, 4096),
-                              ("c3_m64", "q4_0", 64, 4096, 4096)]:
+                              ("c3_m64", "q4_0", 64, 4096, 4096),
+                              ("c3_m16_q8_0", "q8_0", 16, 4096, 4096),
+                              ("c3_m64_q8_0", "q8_0", 64, 4096, 4096),
+                              ("c3_m16_q4_1", "q4_1", 16, 4096, 4096),
+                              ("c3_m64_q4_1", "q4_1", 64, 4096, 4096)]:
         r = bench_case(pkg, torch, qt, m, n, k, args.steps, args.warmup, 100)
         extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
                        for kk, v in r.items()}
         extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+    # configs[4]'s decode sweep: 196 GEMVs of one Qwen2-7B decode step
+    for mode, key in (("separate", "sweep"), ("fused", "sweep_fused"),
+                      ("epilogue", "sweep_epilogue")):
+        sw = bench_sweep(pkg, torch, max(1, args.steps // 100), 1, mode)
+        sw["frac_hbm"] = round(sw["gbs"] / HBM_PEAK_GBS, 4)
+        extra[key] = {kk: (round(v, 3) if isinstance(v, float) else v)
+                      for kk, v in sw.items()}
+    # the one-launch read ceiling at the headline's weight bytes
+    rc = bench_read_ceiling(pkg, torch, args.steps, args.warmup, sizes=READ_SIZES[1:2])
+    result["roofline"]["read_ceiling"] = {
+        "gbs": rc[READ_SIZES[1][0]]["gbs"], "bytes": rc[READ_SIZES[1][0]]["bytes"],
+        "asymptote_gbs_1gib": rc["1 GiB"]["gbs"],
+        "frac_of_ceiling": round(head["gbs"] / rc[READ_SIZES[1][0]]["gbs"], 4),
+        "probe": "mlq_read_probe: streaming dwordx4 read of the same bytes, one launch"}
     result["configs"] = extra
     if args.all:
-        for mode, key in (("separate", "sweep"), ("fused", "sweep_fused"),
-                          ("epilogue", "sweep_epilogue")):
-            sw = bench_sweep(pkg, torch, max(1, args.steps // 100), 1, mode)
-            sw["frac_hbm"] = round(sw["gbs"] / HBM_PEAK_GBS, 4)
-            extra[key] = {kk: (round(v, 3) if isinstance(v, float) else v)
-                          for kk, v in sw.items()}
         gl = bench_gguf_load(pkg, torch)
         extra["gguf_load"] = {kk: (round(v, 3) if isinstance(v, float) else v)
                               for kk, v in gl.items()}
         result["configs"] = extra
     if not args.no_cpu:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline("q4_0", 18944, 3584, args.cpu_budget)
+        cpu = host_cpu()
+        threads = cpu_threads(cpu)
+        result["cpu_baseline"] = cpu_baseline("q4_0", 18944, 3584, args.cpu_budget,
+                                              threads=threads)
         result["cpu_baseline"]["value"] = round(result["cpu_baseline"]["value"], 3)
+        result["cpu_baseline"]["lscpu"] = cpu
+        result["cpu_baseline"]["threads_rule"] = (
+            f"one per physical core, capped at the job's {CPU_SHARE}-thread CPU share")
+        # the same build at 1 thread and half the threads: how the rate scales
+        curve = {}
+        for t in sorted({1, max(1, threads // 2)} - {threads}):
+            v = cpu_baseline("q4_0", 18944, 3584, min(3.0, args.cpu_budget), threads=t)
+            curve[str(t)] = round(v["value"], 3)
+        curve[str(threads)] = result["cpu_baseline"]["value"]
+        result["cpu_baseline"]["gbs_by_threads"] = curve
         # the same CPU path with and without the reference's AVX2 build, on
         # the headline shape and on configs[0] (q8_0, the type with an AVX2
         # loop), a few seconds each
@@ -526,7 +686,7 @@ def main():
             for flavor in ("scalar", "avx2"):
                 if (qt, flavor) == ("q4_0", "scalar") or not oracle.flavor_available(flavor):
                     continue
-                v = cpu_baseline(qt, n, k, min(3.0, args.cpu_budget), flavor)
+                v = cpu_baseline(qt, n, k, min(3.0, args.cpu_budget), flavor, threads)
                 variants.append({"config": tag, "build": flavor,
                                  "value": round(v["value"], 3), "unit": "GB/s",
                                  "cores": v["cores"], "sample": v["sample"]})

@@ -276,6 +276,14 @@ int mlq_set_skinny_plan(int tiles, int splits);
 int mlq_linear_epi_noalloc(const mlq_weight* w, const float* x, float* y, int m,
                            const float* bias, int act, mlq_stream_t stream);
 
+/* Measurement aid, no counterpart in the reference: one streaming read of
+ * `bytes` (a multiple of 16, 16-byte aligned device pointer) in one launch,
+ * dwordx4 loads in 8 KiB chunks per wave, non-temporal like the GEMV's
+ * weight lines; sink is one device word written only by chance. Timing it
+ * at the byte count of a Linear gives the HBM read ceiling of a single
+ * launch of that size (launch ramp and drain included). */
+int mlq_read_probe(const void* p, size_t bytes, uint32_t* sink, mlq_stream_t stream);
+
 /* Add bias[n] to every row of y[m, n] on the device (the reference adds the
  * bias on the host after download, src/cuda_quant.cu:229-235, 327-329). */
 int mlq_add_bias(float* y, const float* bias, int m, int n,

@@ -140,6 +140,7 @@ SIGNATURES = {
     "mlq_gguf_data": ([_P, ctypes.c_int64], _P),
     "mlq_gguf_upload": ([_P, ctypes.c_int64, _P, _Z, _WP, _P], _I),
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
+    "mlq_read_probe": ([_P, _Z, _P, _P], _I),
     "mlq_set_gemv_split": ([_I], _I),
     "mlq_set_gemm_split": ([_I], _I),
     "mlq_set_skinny_plan": ([_I, _I], _I),
@@ -528,6 +529,13 @@ def linear_aos(qtype: str, aos_dev, n: int, k: int, x, workspace=None,
                                 workspace.numel(), _stream(stream)),
            "mlq_linear_aos")
     return y
+
+
+def read_probe(buf, nbytes: int, sink, stream=None) -> None:
+    """mlq_read_probe: one streaming read of the first nbytes of a device
+    tensor (measurement aid)."""
+    _check(lib().mlq_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), _stream(stream)),
+           "mlq_read_probe")
 
 
 def set_gemv_split(split: int = 0) -> None:

@@ -336,6 +336,12 @@ int mlq_set_gemv_split(int split) {
   return MLQ_OK;
 }
 
+int mlq_read_probe(const void* p, size_t bytes, uint32_t* sink, mlq_stream_t stream) {
+  if (p == nullptr || sink == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (bytes == 0 || bytes % 16 != 0 || ((uintptr_t)p & 15) != 0) return MLQ_ERR_SHAPE;
+  return hip_status(launch_read_probe(p, bytes, sink, (hipStream_t)stream));
+}
+
 int mlq_add_bias(float* y, const float* bias, int m, int n,
                  mlq_stream_t stream) {
   if (y == nullptr || bias == nullptr) return MLQ_ERR_INVALID_ARG;

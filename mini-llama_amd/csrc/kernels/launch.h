@@ -124,6 +124,9 @@ hipError_t launch_skinny_ws(const mlq_weight& w, const float* x, float* y, int m
 // ranges per tile group (1..8); validated by the caller.
 void set_skinny_plan(int tiles, int splits);
 
+// probe.hip: streaming read of `bytes` at p (sink: one device word).
+hipError_t launch_read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t stream);
+
 // linear_f32.hip: fp32 W [n][k], any m (passes of up to 8 rows).
 hipError_t launch_linear_f32(const float* w, int n, int k, const float* x, float* y, int m,
                              hipStream_t stream, const Epilogue& epi = Epilogue());

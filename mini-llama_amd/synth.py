@@ -118,7 +118,7 @@ def synthetic_model(config: dict, qtype: str = "q4_0", seed: int = 0,
             "layers": layers}
 
 
-def _device_blocks(torch, gen, qtype: str, n: int, k: int, rms: float, device):
+def device_blocks(torch, gen, qtype: str, n: int, k: int, rms: float, device):
     """GGUF block bytes made on the device (same distributions as
     make_blocks_scaled), [n * ceil(k/32) * block bytes] uint8."""
     count = n * ((k + 31) // 32)
@@ -159,7 +159,7 @@ def synthetic_model_device(config: dict, qtype: str = "q4_0", seed: int = 0,
             return {"type": "f32", "shape": (n, k),
                     "data": torch.randn(n, k, generator=gen, device=device) * rms}
         return {"type": qtype, "shape": (n, k),
-                "data": _device_blocks(torch, gen, qtype, n, k, rms, device)}
+                "data": device_blocks(torch, gen, qtype, n, k, rms, device)}
 
     def norm():
         return 1.0 + 0.1 * torch.randn(dim, generator=gen, device=device)

@@ -479,6 +479,20 @@ def test_bias_kernel(pkg, cuda):
                           np.array([1.0, -2.0, 0.5, 4.0], np.float32))
 
 
+def test_read_probe_runs_in_bounds(pkg, cuda):
+    """The bench's read probe over whole and ragged sizes (a partial last
+    8 KiB chunk, a partial last block of waves): it completes, and on data
+    that fold to zero it leaves the sink word untouched."""
+    torch = _torch()
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device=cuda)
+    sink = torch.full((1,), 7, dtype=torch.int32, device=cuda)
+    for nbytes in (16, 8192, 8192 + 48, 3 * 8192 * 4 + 16, 1 << 20):
+        print(f"read probe {nbytes} B", flush=True)
+        pkg.read_probe(buf, nbytes, sink)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 7
+
+
 def test_validation_errors(pkg, cuda):
     torch = _torch()
     blocks = make_blocks("q4_0", 16, 64, seed=1)
