@@ -137,17 +137,19 @@ int mlq_linear(const mlq_weight* w, const float* x, float* y, int m,
 
 /* Device workspace bytes mlq_linear_ws needs for m activation rows with
  * weight w (*bytes = 0 when the kernels for that shape need none: the decode
- * GEMV). The skinny and prefill GEMMs use it for a one-pass fp16 copy of x,
- * which halves the activation bytes their stages move; the prefill GEMM
- * also for fp32 partial outputs when it splits K across workgroups (shapes
- * with few output tiles). The size depends on the shape, the split-K
- * override and the device's compute-unit count. */
+ * GEMV, and 9..16 rows with k <= 6144, k % 4 == 0, whose skinny kernel reads
+ * fp32 x itself). The skinny (17..64 rows, or longer rows) and prefill
+ * GEMMs use it for a one-pass fp16 copy of x, which halves the activation
+ * bytes their stages move; both also for fp32 partial outputs when they
+ * split K across workgroups (shapes with few output tiles). The size
+ * depends on the shape, the split-K overrides and the device's
+ * compute-unit count. */
 int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes);
 
 /* mlq_linear with a caller workspace of at least mlq_linear_workspace(w, m)
  * bytes (device memory, 256-byte aligned; contents need no initialisation
- * and are scratch for the duration of the call). MLQ_ERR_BUFFER_TOO_SMALL
- * when it is smaller. Calls that share one workspace must be ordered (same
+ * and are scratch for the duration of the call; may be NULL when that size
+ * is 0). MLQ_ERR_BUFFER_TOO_SMALL when it is smaller. Calls that share one workspace must be ordered (same
  * stream), like any other buffer. Same result contract as mlq_linear (fp16
  * rounding of x happens in both prefill variants). No counterpart in the
  * reference (its kernels take fp32 x directly, src/cuda_quant.cu:78-182). */

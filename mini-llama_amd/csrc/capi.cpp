@@ -265,10 +265,11 @@ int mlq_linear_epi(const mlq_weight* w, const float* x, float* y, int m,
   if (uses_gemv(w, m)) return hip_status(launch_gemv(*w, x, y, m, s, epi));
   const size_t need = m <= kSkinnyMaxRows ? skinny_workspace_bytes(w->type, m, w->n, w->k)
                                            : gemm_workspace_bytes(m, w->n, w->k);
-  if (workspace == nullptr || workspace_bytes < need)
-    return MLQ_ERR_BUFFER_TOO_SMALL;
-  if (((uintptr_t)workspace & 255u) != 0) return MLQ_ERR_INVALID_ARG;
-  if (m <= kSkinnyMaxRows)  // batched decode: fp16 x copy, skinny GEMM
+  if (need > 0) {
+    if (workspace == nullptr || workspace_bytes < need) return MLQ_ERR_BUFFER_TOO_SMALL;
+    if (((uintptr_t)workspace & 255u) != 0) return MLQ_ERR_INVALID_ARG;
+  }
+  if (m <= kSkinnyMaxRows)  // batched decode: skinny GEMM (+ split-K reduce)
     return hip_status(launch_skinny_ws(*w, x, y, m, workspace, workspace_bytes, s, epi));
   return hip_status(launch_gemm_ws(*w, x, y, m, workspace, workspace_bytes, s, epi));
 }

@@ -110,10 +110,11 @@ hipError_t launch_split_reduce(const float* part, float* y, int m, int n, int sp
                                const GemmOut& out = GemmOut());
 
 // skinny.hip: 9..64 rows of x. launch_skinny_ws makes the fragment-ordered
-// fp16 copy of x in ws, then runs the skinny GEMM (K split over
-// workgroups when the planner chooses it: counters and partial slices
-// after the copy); ws holds skinny_workspace_bytes(type, m, n, k) bytes,
-// 256-byte aligned.
+// fp16 copy of x in ws (not for 9..16 rows with k <= 6144, k % 4 == 0:
+// that kernel reads fp32 x itself), then runs the skinny GEMM (K split over
+// workgroups when the planner chooses it: partial slices after the copy);
+// ws holds skinny_workspace_bytes(type, m, n, k) bytes, 256-byte aligned
+// (may be null when that is 0).
 constexpr int kSkinnyMaxRows = 64;
 size_t skinny_x_bytes(int m, int k);
 size_t skinny_workspace_bytes(int type, int m, int n, int k);
