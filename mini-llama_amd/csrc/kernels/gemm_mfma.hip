@@ -376,8 +376,13 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
   }
   __syncthreads();
 
+  // q8_0 two workgroups per CU: A fragments read in their own k step (the
+  // other workgroup hides the LDS latency) instead of one step ahead; the
+  // 16 registers this frees keep the kernel within 256 without spills (a
+  // spill reload in the loop waits for every outstanding load)
+  constexpr bool kPrefA = !(OCC == 2 && QT == MLQ_Q8_0);
   h8_t af[4], bf[2];
-  read_a(af, 0, 0);
+  if constexpr (kPrefA) read_a(af, 0, 0);
 #pragma unroll
   for (int j = 0; j < 2; ++j) bf[j] = decode_w<QT>(ws[0], j, 0);
 
@@ -394,16 +399,17 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
     constexpr int BC = S % 3, BN = (S + 1) % 3, BA = (S + 2) % 3;
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
+      if constexpr (!kPrefA) read_a(af, BC, ks);
       if (ks == 0) lx(xs[XA], min(s + kXS + 1, last));
       if (ks == 1) lw(ws[WA], min(s + 2, last));
       h8_t an[4], bn[2];
       if (ks < kBK / 16 - 1) {
-        read_a(an, BC, ks + 1);
+        if constexpr (kPrefA) read_a(an, BC, ks + 1);
 #pragma unroll
         for (int j = 0; j < 2; ++j) bn[j] = decode_w<QT>(ws[WC], j, ks + 1);
       } else {
         if (s + 2 < stages) sx(xs[XC], BA, s + 2);
-        read_a(an, BN, 0);
+        if constexpr (kPrefA) read_a(an, BN, 0);
 #pragma unroll
         for (int j = 0; j < 2; ++j) bn[j] = decode_w<QT>(ws[WN], j, 0);
       }
@@ -429,8 +435,10 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_kernel(GemmArgs a) {
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kPrefA) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = an[i];
+        for (int i = 0; i < 4; ++i) af[i] = an[i];
+      }
 #pragma unroll
       for (int j = 0; j < 2; ++j) bf[j] = bn[j];
     }
