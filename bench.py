@@ -34,7 +34,8 @@ reference that scales the FETCH_SIZE / WRITE_SIZE counters to bytes;
 `--mode case --case qtype,m,n,k` launches one Linear shape (the skinny and
 prefill GEMM counter summaries in profiles/ come from it), `--mode
 read-ceiling` times the read probe at every BASELINE weight size and
-`--mode sweep` the three 196-GEMV sweeps alone.
+`--mode sweep` the three 196-GEMV sweeps alone. `configs.c1_aos` /
+`c0_aos` time mlq_linear_aos on raw GGUF blocks (the direct AoS GEMV).
 `roofline.traffic` is read from profiles/hbm_traffic_gemv_q4_0_c1.md (the
 summary of those counter runs) when it is present, else null.
 """
@@ -243,6 +244,41 @@ def bench_sweep(pkg, torch, steps, warmup, mode):
     log(f"sweep ({mode}): {sec * 1e6:.1f} us/step, {total / sec / 1e9:.0f} GB/s")
     return {"gemvs": 196, "launches": launches, "us_per_step": sec * 1e6,
             "gbs": total / sec / 1e9, "bytes": total, "tflops": flops / sec / 1e12}
+
+
+def bench_aos(pkg, torch, qtype, m, n, k, steps, warmup, seed):
+    """mlq_linear_aos on raw GGUF blocks (the reference's device-weight
+    meaning), rotated over >= 512 MB of copies: the direct AoS GEMV (m <= 8,
+    no workspace) or the repack + tiled kernels."""
+    import ctypes
+    import mini_llama_amd.synth as synth
+    blocks = synth.make_blocks(qtype, n, k, seed)
+    raw = pkg.upload_aos(blocks, device="cuda")
+    copies = max(1, -(-ROTATE_BYTES // raw.numel()))
+    bufs = [raw] + [raw.clone() for _ in range(copies - 1)]
+    x = torch.from_numpy(synth.make_x(m, k, seed + 1)).to("cuda")
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    need = pkg.aos_workspace_bytes(qtype, n, k, m)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    lib, t, bb = pkg.lib(), pkg.TYPES[qtype], pkg.BLOCK_BYTES[qtype]
+
+    def launch(i):
+        b = bufs[i % len(bufs)]
+        rc = lib.mlq_linear_aos(t, b.data_ptr(), b.numel() // bb, n, k, x.data_ptr(),
+                                y.data_ptr(), m, ws.data_ptr() if need else None, need,
+                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0, rc
+    sec = time_graph(torch, launch, steps, warmup) / steps
+    assert torch.isfinite(y).all().item()
+    out = {"qtype": qtype, "m": m, "n": n, "k": k, "copies": len(bufs),
+           "path": "direct AoS GEMV" if need == 0 else "repack + tiled",
+           "us_per_call": round(sec * 1e6, 3),
+           "gbs": round(alg_bytes(qtype, m, n, k) / sec / 1e9, 1)}
+    out["frac_hbm"] = round(out["gbs"] / HBM_PEAK_GBS, 4)
+    log(f"aos {qtype} m={m} n={n} k={k}: {out['us_per_call']} us ({out['path']})")
+    del bufs, raw
+    torch.cuda.empty_cache()
+    return out
 
 
 READ_SIZES = [("c0 q8_0 4096x4096", "q8_0", 4096, 4096),
@@ -639,6 +675,12 @@ def main():
         extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
                        for kk, v in r.items()}
         extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+    # raw GGUF block pointers (mlq_linear_aos, the reference's device-weight
+    # meaning) at configs[1] and configs[0]
+    extra["c1_aos"] = bench_aos(pkg, torch, "q4_0", 1, 18944, 3584, args.steps,
+                                args.warmup, 1000)
+    extra["c0_aos"] = bench_aos(pkg, torch, "q8_0", 1, 4096, 4096, args.steps,
+                                args.warmup, 100)
     # configs[4]'s decode sweep: 196 GEMVs of one Qwen2-7B decode step
     for mode, key in (("separate", "sweep"), ("fused", "sweep_fused"),
                       ("epilogue", "sweep_epilogue")):

@@ -223,12 +223,21 @@ int mlq_gguf_upload(const mlq_gguf* g, int64_t index, void* aos_dev, size_t aos_
 
 /* Raw GGUF AoS blocks in device memory: the meaning of the `const void*`
  * weight of cudaQ*LinearDeviceWeight / cudaQ*LinearDeviceInput
- * (src/cuda_quant.cu:300-361). The blocks are repacked into `workspace`
- * (device, >= mlq_weight_layout(...).bytes) and then run through
- * mlq_linear. */
+ * (src/cuda_quant.cu:300-361). Up to 8 rows of x whose k fits the kernel's
+ * LDS staging (mlq_linear_aos_workspace reports 0 bytes) run a GEMV that
+ * reads the blocks as they are, every weight byte once; `workspace` may
+ * then be NULL. Otherwise the blocks are repacked into `workspace` (device,
+ * >= mlq_weight_layout(...).bytes) and run through mlq_linear. Results
+ * meet the Linear's tolerance either way (the direct GEMV sums in fp32
+ * like the reference's per-element loop, in another order). */
 int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,
                    int k, const float* x, float* y, int m, void* workspace,
                    size_t workspace_bytes, mlq_stream_t stream);
+
+/* Workspace bytes mlq_linear_aos needs for m rows: 0 when the direct GEMV
+ * takes the shape, the tiled layout's bytes otherwise. No counterpart in
+ * the reference. */
+int mlq_linear_aos_workspace(int type, int n, int k, int m, size_t* bytes);
 
 /* Kernel-family overrides for tests and measurement: force the GEMV
  * (requires m <= 8 and k within its LDS budget, else MLQ_ERR_UNSUPPORTED)

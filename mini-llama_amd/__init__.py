@@ -123,6 +123,7 @@ SIGNATURES = {
     "mlq_dequantize": ([_WP, _I, _I, _P, _P], _I),
     "mlq_linear": ([_WP, _P, _P, _I, _P], _I),
     "mlq_linear_aos": ([_I, _P, _Z, _I, _I, _P, _P, _I, _P, _Z, _P], _I),
+    "mlq_linear_aos_workspace": ([_I, _I, _I, _I, _P], _I),
     "mlq_linear_path": ([_WP, _P, _P, _I, _I, _P], _I),
     "mlq_linear_workspace": ([_WP, _I, ctypes.POINTER(_Z)], _I),
     "mlq_linear_ws": ([_WP, _P, _P, _I, _P, _Z, _P], _I),
@@ -511,22 +512,32 @@ def linear_noalloc(w: TiledWeight, x, y=None, bias=None, act: int = EPI_NONE,
     return y
 
 
+def aos_workspace_bytes(qtype: str, n: int, k: int, m: int) -> int:
+    """mlq_linear_aos_workspace: 0 when the direct AoS GEMV takes the shape."""
+    nbytes = ctypes.c_size_t(0)
+    _check(lib().mlq_linear_aos_workspace(TYPES[qtype], n, k, m, ctypes.byref(nbytes)),
+           "mlq_linear_aos_workspace")
+    return nbytes.value
+
+
 def linear_aos(qtype: str, aos_dev, n: int, k: int, x, workspace=None,
                stream=None):
-    """Linear on raw GGUF blocks in device memory (repacked into workspace)."""
+    """Linear on raw GGUF blocks in device memory: up to 8 rows read the
+    blocks as they are, otherwise they are repacked into a workspace."""
     import torch
     m = 1 if x.dim() == 1 else x.shape[0]
-    layout = weight_layout(qtype, n, k)
-    if workspace is None:
-        workspace = torch.empty(int(layout.bytes), dtype=torch.uint8,
-                                device=x.device)
+    need = aos_workspace_bytes(qtype, n, k, m)
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     y = torch.empty((n,) if x.dim() == 1 else (m, n), dtype=torch.float32,
                     device=x.device)
     bb = BLOCK_BYTES[qtype]
     _check(lib().mlq_linear_aos(TYPES[qtype], aos_dev.data_ptr(),
                                 aos_dev.numel() // bb, n, k, x.data_ptr(),
-                                y.data_ptr(), m, workspace.data_ptr(),
-                                workspace.numel(), _stream(stream)),
+                                y.data_ptr(), m,
+                                workspace.data_ptr() if workspace is not None else None,
+                                workspace.numel() if workspace is not None else 0,
+                                _stream(stream)),
            "mlq_linear_aos")
     return y
 

@@ -298,14 +298,27 @@ int mlq_interleave_rows(const void* gate, const void* up, int rows,
   return MLQ_OK;
 }
 
+int mlq_linear_aos_workspace(int type, int n, int k, int m, size_t* bytes) {
+  if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (n <= 0 || k <= 0 || m <= 0) return MLQ_ERR_SHAPE;
+  mlq_weight w;
+  const int rc = mlq_weight_layout(type, n, k, &w);
+  if (rc != MLQ_OK) return rc;
+  *bytes = aos_gemv_supported(type, m, n, k) ? 0 : (size_t)w.bytes;
+  return MLQ_OK;
+}
+
 int mlq_linear_aos(int type, const void* aos_dev, size_t block_count, int n,
                    int k, const float* x, float* y, int m, void* workspace,
                    size_t workspace_bytes, mlq_stream_t stream) {
   int rc = check_weight(type, block_count, n, k);
   if (rc != MLQ_OK) return rc;
-  if (aos_dev == nullptr || x == nullptr || y == nullptr || workspace == nullptr)
-    return MLQ_ERR_INVALID_ARG;
+  if (aos_dev == nullptr || x == nullptr || y == nullptr) return MLQ_ERR_INVALID_ARG;
   if (m <= 0) return MLQ_ERR_SHAPE;
+  // up to 8 rows whose x fits in LDS: one pass over the blocks as they are
+  if (aos_gemv_supported(type, m, n, k))
+    return hip_status(launch_aos_gemv(type, aos_dev, n, k, x, y, m, (hipStream_t)stream));
+  if (workspace == nullptr) return MLQ_ERR_INVALID_ARG;
   mlq_weight w;
   mlq_weight_layout(type, n, k, &w);
   if (workspace_bytes < w.bytes) return MLQ_ERR_BUFFER_TOO_SMALL;

@@ -116,12 +116,15 @@ void runLinear(int type, const void* w_dev, size_t block_count,
     if (ws_bytes) ws = deviceWorkspace(kActivationWorkspace, device_id, ws_bytes);
     rc = mlq_linear_ws(&layout, x, y, p.rows, ws.data, ws_bytes, nullptr);
   } else {
-    mlq_weight need;
-    rc = mlq_weight_layout(type, p.out_features, p.in_features, &need);
+    // GGUF blocks as they are: up to 8 rows read them directly (no
+    // workspace), more are repacked into the per-device workspace first
+    size_t need = 0;
+    rc = mlq_linear_aos_workspace(type, p.out_features, p.in_features, p.rows, &need);
     checkStatus(rc, caller);
-    Workspace ws = deviceWorkspace(kAosWorkspace, device_id, need.bytes);
+    Workspace ws;
+    if (need) ws = deviceWorkspace(kAosWorkspace, device_id, need);
     rc = mlq_linear_aos(type, w_dev, block_count, p.out_features, p.in_features,
-                        x, y, p.rows, ws.data, need.bytes, nullptr);
+                        x, y, p.rows, ws.data, need, nullptr);
   }
   checkStatus(rc, "mlq_linear");
 }

@@ -125,6 +125,12 @@ hipError_t launch_skinny_ws(const mlq_weight& w, const float* x, float* y, int m
 // ranges per tile group (1..8); validated by the caller.
 void set_skinny_plan(int tiles, int splits);
 
+// aos_gemv.hip: GEMV straight from GGUF AoS blocks (m <= 8 rows of x, x
+// staged in LDS: aos_gemv_supported says whether the shape fits).
+bool aos_gemv_supported(int type, int m, int n, int k);
+hipError_t launch_aos_gemv(int type, const void* aos, int n, int k, const float* x, float* y,
+                           int m, hipStream_t stream);
+
 // probe.hip: streaming read of `bytes` at p (sink: one device word).
 hipError_t launch_read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t stream);
 

@@ -315,9 +315,13 @@ TEST(hip_uploaded_weight_matches_aos_pointer) {
       hipQ40LinearDeviceInput(xd, aos.data(), qt.q4_0_data.size(), qt.shape, 0)
           .download();
   Tensor cpu = cpuLinear(x, qt.q4_0_data, qt.shape);
-  CHECK(expectNear(via_registry, via_aos, 0.0f, "registry vs aos (bit-exact)"));
-  CHECK(expectNear(via_uploaded, via_aos, 0.0f, "uploaded vs aos (bit-exact)"));
-  CHECK(expectNear(via_aos, cpu, 1e-4f, "aos vs cpu"));
+  // a registered buffer runs the tiled kernels; a raw AoS pointer (3 rows)
+  // runs the GEMV that reads the blocks as they are, in fp32 like the CPU
+  // loop but in another summation order
+  CHECK(expectNear(via_registry, via_uploaded, 0.0f, "registry vs uploaded (bit-exact)"));
+  CHECK(expectNear(via_registry, via_aos, 1e-5f, "registry vs aos"));
+  CHECK(expectNear(via_aos, cpu, 1e-5f, "aos vs cpu"));
+  CHECK(expectNear(via_registry, cpu, 1e-4f, "registry vs cpu"));
   return true;
 }
 

@@ -211,9 +211,53 @@ def test_linear_1d_input_and_aos_path(pkg, oracle, cuda, qtype):
     assert y_tiled.shape == (n,)
     y_aos = pkg.linear_aos(qtype, pkg.upload_aos(blocks, device=cuda), n, k,
                            _dev(x, cuda)).cpu().numpy()
-    assert np.array_equal(y_tiled, y_aos)  # same kernels, same bits
     ref = oracle.linear(x, blocks, (n, k), qtype)
     assert tolerance_ok(y_tiled, ref, x[None], k).all()
+    assert tolerance_ok(y_aos, ref, x[None], k).all()
+
+
+AOS_SHAPES = [  # (m, n, k): direct GEMV (m <= 8, x fits LDS) and repack fallback
+    (1, 80, 544), (3, 17, 1001), (1, 4096, 4096), (1, 33, 18944), (8, 70, 300),
+    (8, 40, 3000), (2, 300, 97), (8, 40, 4000), (9, 40, 256)]
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("m,n,k", AOS_SHAPES)
+def test_aos_direct_gemv(pkg, oracle, cuda, qtype, m, n, k):
+    """Raw GGUF blocks (the reference's `const void*` device weight,
+    src/cuda_quant.cu:300-361): up to 8 rows whose x fits in LDS read the
+    blocks as they are (no workspace), with the reference's fp32
+    per-element arithmetic in another order: within 1e-5 of max|y| of the
+    oracle, and the stated bar; rows that start at any 2-byte offset (odd
+    block counts, a base pointer 2 / 6 / 10 bytes past alignment); larger
+    shapes take the repack and match the tiled kernels bit for bit."""
+    torch = _torch()
+    _print_case(test="aos_direct", qtype=qtype, m=m, n=n, k=k)
+    blocks = make_blocks(qtype, n, k, seed=3 * n + k + m)
+    x = make_x(m, k, seed=k + 5)
+    xd = _dev(x if m > 1 else x[0], cuda)
+    ref = oracle.linear(x, blocks, (n, k), qtype, threads=8)
+    need = pkg.aos_workspace_bytes(qtype, n, k, m)
+    direct = m <= 8 and need == 0
+    raw = np.ascontiguousarray(blocks).view(np.uint8).reshape(-1)
+    for lead in (0, 2, 6, 10):
+        buf = torch.zeros(raw.size + 16, dtype=torch.uint8, device=cuda)
+        buf[lead:lead + raw.size] = torch.from_numpy(raw).to(cuda)
+        aos = buf[lead:lead + raw.size]
+        y = np.atleast_2d(pkg.linear_aos(qtype, aos, n, k, xd).cpu().numpy())
+        assert tolerance_ok(y, ref, x, k).all(), (lead, error_report(y, ref, x, k))
+        if direct:
+            scale = np.abs(ref).max() + 1e-30
+            assert np.abs(y - ref).max() <= 1e-5 * scale, (lead, np.abs(y - ref).max() / scale)
+        else:
+            tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+            want = np.atleast_2d(pkg.linear(tw, xd, path=pkg.PATH_AUTO,
+                                            workspace=None).cpu().numpy())
+            assert np.array_equal(y, want), lead
+        again = np.atleast_2d(pkg.linear_aos(qtype, aos, n, k, xd).cpu().numpy())
+        assert np.array_equal(y, again)
+    if m <= 8 and k <= 3000:
+        assert direct, (m, n, k, need)
 
 
 @pytest.mark.parametrize("qtype", TYPES)
