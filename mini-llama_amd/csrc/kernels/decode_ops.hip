@@ -973,10 +973,8 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
   // global max and sum in one pass over the partials: each lane keeps a
   // running (max, sum rescaled to it), then the lanes' pairs are merged
   float mx = -INFINITY, ls = 0.0f;
-  float m_first = -INFINITY;  // pm[lane]: the first batch's weight of this lane
   for (int c = lane; c < chunks; c += 64) {
     const float m = pm[c], l = pl[c];
-    if (c == lane) m_first = m;
     const float nm = fmaxf(mx, m);
     ls = (mx == -INFINITY ? 0.0f : ls * expf(mx - nm)) + (m == -INFINITY ? 0.0f : l * expf(m - nm));
     mx = nm;
@@ -992,7 +990,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
     const int nc = min(kCombineBatch, chunks - c0);
     __syncthreads();
     if (lane < kCombineBatch) {
-      const float m = c0 == 0 ? m_first : (lane < nc ? pm[c0 + lane] : -INFINITY);
+      const float m = lane < nc ? pm[c0 + lane] : -INFINITY;
       wsh[lane] = lane < nc ? expf(m - mx) : 0.0f;
     }
     __syncthreads();

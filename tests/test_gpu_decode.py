@@ -225,8 +225,7 @@ def test_attention_reference_cases(pkg, oracle, cuda):
     (14, 2, 64, 300, 200), (7, 1, 256, 200, 150), (21, 3, 96, 100, 60),
     # more than 128 chunk partials per head: the combine's online max/sum
     # runs over several chunks per lane, and its weighted sum over more than
-    # one 32-chunk batch (the first batch from the maxima pass, later ones
-    # reloaded)
+    # one 32-chunk batch
     (8, 2, 128, 9100, 9000), (6, 3, 96, 4600, 4500)])
 def test_attention_matches_oracle(pkg, oracle, cuda, n_heads, n_kv, hd, max_seq, pos):
     rng = np.random.default_rng(pos * 7 + hd)
