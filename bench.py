@@ -34,7 +34,8 @@ reference that scales the FETCH_SIZE / WRITE_SIZE counters to bytes;
 `--mode case --case qtype,m,n,k` launches one Linear shape (the skinny and
 prefill GEMM counter summaries in profiles/ come from it), `--mode
 read-ceiling` times the read probe at every BASELINE weight size and
-`--mode sweep` the three 196-GEMV sweeps alone. `configs.c1_aos` /
+`--mode sweep` the three 196-GEMV sweeps alone, `--mode skinny-floor` the
+load-only floors of the skinny GEMM's access pattern (mlq_read_probe_shared). `configs.c1_aos` /
 `c0_aos` time mlq_linear_aos on raw GGUF blocks (the direct AoS GEMV).
 `roofline.traffic` is read from profiles/hbm_traffic_gemv_q4_0_c1.md (the
 summary of those counter runs) when it is present, else null.
@@ -324,6 +325,45 @@ def bench_read_ceiling(pkg, torch, steps, warmup, sizes=None):
     return out
 
 
+SKINNY_FLOOR_CASES = [  # (name, shared bytes per workgroup, own bytes per wave)
+    ("weights 36 KiB/WG", 0, 4608),
+    ("x 128 KiB/WG", 128 << 10, 0),
+    ("x 256 KiB/WG", 256 << 10, 0),
+    ("weights + x fp16 M=16 (128 KiB)", 128 << 10, 4608),
+    ("weights + x fp32 M=16 (256 KiB)", 256 << 10, 4608),
+    ("weights + x fp16 M=4..8 (64 KiB)", 64 << 10, 4608),
+]
+
+
+def bench_skinny_floor(pkg, torch, steps, warmup):
+    """Load-only floors of the skinny GEMM's pattern at q4_0 W[4096, 4096]
+    (configs[3]): mlq_read_probe_shared with 256 workgroups of 8 waves, each
+    workgroup streaming its 36 KiB weight tile from HBM (rotated over a
+    >= 512 MB pool) and/or reading the same x region (resident in L2 / the
+    Infinity Cache after the first launch). Timed as one HIP graph."""
+    wgs = 256
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    shared = torch.ones(256 << 10, dtype=torch.uint8, device="cuda")
+    out = {}
+    for name, sb, opw in SKINNY_FLOOR_CASES:
+        per = max(opw, 16) * 8 * wgs
+        stride = -(-per // 4096) * 4096
+        slots = max(2, -(-ROTATE_BYTES // stride) + 1)
+        pool = torch.zeros(slots * stride, dtype=torch.uint8, device="cuda")
+        views = [pool[i * stride:i * stride + per] for i in range(slots)]
+
+        def launch(i):
+            pkg.read_probe_shared(shared, sb, views[i % slots], opw, wgs, sink)
+        sec = time_graph(torch, launch, steps, warmup) / steps
+        out[name] = {"shared_bytes": sb, "own_bytes_per_wave": opw,
+                     "us": round(sec * 1e6, 3)}
+        log(f"skinny floor {name}: {sec * 1e6:.2f} us")
+        del views, pool
+        torch.cuda.empty_cache()
+    assert int(sink.item()) == 0
+    return out
+
+
 def bench_gguf_load(pkg, torch, layers=4):
     """Weight load from a GGUF file: `layers` Qwen2-7B layers (q4_0, 7
     Linear tensors each, ~131 MB per layer) written to a temporary file,
@@ -561,7 +601,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--mode", choices=["full", "headline", "copy", "decode", "case",
-                                       "read-ceiling", "sweep"],
+                                       "read-ceiling", "sweep", "skinny-floor"],
                     default="full", help="headline/copy/decode/case: profiling runs")
     ap.add_argument("--case", default="q4_0,16,4096,4096",
                     help="--mode case: qtype,m,n,k of the one shape to launch")
@@ -597,6 +637,10 @@ def main():
     if args.mode == "read-ceiling":
         r = bench_read_ceiling(pkg, torch, args.steps, args.warmup)
         print(json.dumps({"mode": "read-ceiling", "sizes": r}), flush=True)
+        return
+    if args.mode == "skinny-floor":
+        r = bench_skinny_floor(pkg, torch, args.steps, args.warmup)
+        print(json.dumps({"mode": "skinny-floor", "cases": r}), flush=True)
         return
     if args.mode == "sweep":
         r = {mode: bench_sweep(pkg, torch, max(1, args.steps // 100), 1, mode)

@@ -133,6 +133,9 @@ hipError_t launch_aos_gemv(int type, const void* aos, int n, int k, const float*
 
 // probe.hip: streaming read of `bytes` at p (sink: one device word).
 hipError_t launch_read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t stream);
+hipError_t launch_shared_probe(const void* shared, size_t shared_bytes, const void* own,
+                               size_t own_per_wave, int workgroups, uint32_t* sink,
+                               hipStream_t stream);
 
 // linear_f32.hip: fp32 W [n][k], any m (passes of up to 8 rows).
 hipError_t launch_linear_f32(const float* w, int n, int k, const float* x, float* y, int m,

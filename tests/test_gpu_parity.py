@@ -551,6 +551,25 @@ def test_read_probe_runs_in_bounds(pkg, cuda):
     assert int(sink.item()) == 7
 
 
+def test_read_probe_shared_runs_in_bounds(pkg, cuda):
+    """The skinny-floor probe at every accepted shared size, with whole and
+    ragged per-wave ranges (a partial last 1 KiB load): it completes, and on
+    zero data it leaves the sink word untouched."""
+    torch = _torch()
+    shared = torch.zeros(256 << 10, dtype=torch.uint8, device=cuda)
+    wgs = 12
+    own = torch.zeros(wgs * 8 * 8192, dtype=torch.uint8, device=cuda)
+    sink = torch.full((1,), 7, dtype=torch.int32, device=cuda)
+    for sb in (0, 64 << 10, 128 << 10, 256 << 10):
+        for opw in (0, 16, 1024, 4608, 8192):
+            if sb == 0 and opw == 0:
+                continue
+            print(f"shared probe shared={sb} own/wave={opw}", flush=True)
+            pkg.read_probe_shared(shared, sb, own, opw, wgs, sink)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 7
+
+
 def test_validation_errors(pkg, cuda):
     torch = _torch()
     blocks = make_blocks("q4_0", 16, 64, seed=1)
