@@ -383,7 +383,25 @@ __device__ __forceinline__ float quad_max_nonneg(float v) {
   return __builtin_bit_cast(float, b);
 }
 
-template <int QT, int T, bool VEC>
+// Largest |x| of four values joined to m; NaN propagates (a NaN row's
+// output is NaN whatever its scale). Two v_maximum3_f32 with abs modifiers.
+__device__ __forceinline__ float abs_maximum4(float m, float4 v) {
+  m = __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, __builtin_fabsf(v.x)),
+                                    __builtin_fabsf(v.y));
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(m, __builtin_fabsf(v.z)),
+                                       __builtin_fabsf(v.w));
+}
+
+// x * 2^e rounded once to fp16 (v_fma_mixlo / mixhi: the scaling is exact,
+// so this is the rounding of the scaled value), two values per word.
+__device__ __forceinline__ uint32_t scale_pack_h2(float a, float b, float s) {
+  h2_t h;
+  h.x = (_Float16)__builtin_fmaf(a, s, 0.0f);
+  h.y = (_Float16)__builtin_fmaf(b, s, 0.0f);
+  return as_u32(h);
+}
+
+template <int QT, int T>
 __global__ __launch_bounds__(kThreads) void skinny_x32_kernel(SkinnyArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kX32Smem];
   const int tid = threadIdx.x;
@@ -414,28 +432,25 @@ __global__ __launch_bounds__(kThreads) void skinny_x32_kernel(SkinnyArgs a) {
   }
   const rsrc_t rx = make_rsrc(a.x, (uint32_t)((size_t)a.m * a.k * 4));
   // quad rho = lane / 4 reads row rho; lane q = lane % 4 the 16 bytes at
-  // column 16 j + 4 q of the chunk (j < 16); columns past the wave's range
-  // and rows past m load zeros (offset 2^31 is past the buffer)
+  // column 16 j + 4 q of the chunk (j < 16). Rows past m start at offset
+  // 2^31, past the buffer (m * k * 4 < 2^31), so every load of theirs reads
+  // zeros; columns past the wave's range load zeros the same way (only the
+  // wave's last chunk can hold any: the check is skipped, wave-uniformly,
+  // for chunks that lie inside the range).
   const int rho = lane >> 2, q = lane & 3;
-  const bool rok = rho < a.m;
+  const uint32_t xl = rho < a.m ? (uint32_t)((rho * a.k + 4 * q) * 4) : 0x80000000u;
   auto load_x = [&](float4 (&xv)[16], int c) __attribute__((always_inline)) {
     const int kb = (g0 + 2 * c) * kGroupK;
+    const uint32_t base = xl + (uint32_t)kb * 4;
+    if (kb + 2 * kGroupK <= kend) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int kc = kb + 16 * j + 4 * q;
-      if constexpr (VEC) {
-        const uint32_t off = rok && kc < kend ? (uint32_t)((rho * a.k + kc) * 4) : 0x80000000u;
+      for (int j = 0; j < 16; ++j)
+        xv[j] = __builtin_bit_cast(float4, buf_load16(rx, base + 64 * j, 0));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t off = kb + 16 * j + 4 * q < kend ? base + 64 * j : 0x80000000u;
         xv[j] = __builtin_bit_cast(float4, buf_load16(rx, off, 0));
-      } else {
-        uint32_t e[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t off =
-              rok && kc + i < kend ? (uint32_t)((rho * a.k + kc + i) * 4) : 0x80000000u;
-          e[i] = buf_load4(rx, off, 0);
-        }
-        xv[j] = make_float4(__builtin_bit_cast(float, e[0]), __builtin_bit_cast(float, e[1]),
-                            __builtin_bit_cast(float, e[2]), __builtin_bit_cast(float, e[3]));
       }
     }
   };
@@ -453,21 +468,23 @@ __global__ __launch_bounds__(kThreads) void skinny_x32_kernel(SkinnyArgs a) {
   // MFMAs run
   auto run = [&](float4 (&xv)[16], const Lines2<QT, T>& w, int c, auto refill)
                  __attribute__((always_inline)) {
-    int ex[2];
+    float sc[2];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
       float mx = 0.0f;
 #pragma unroll
-      for (int j = 8 * gi; j < 8 * gi + 8; ++j) mx = abs_max4(mx, xv[j]);
-      ex[gi] = pow2_scale_exp(quad_max_nonneg(mx));
-      if (q == 0) sexp[gi * 16 + rho] = ex[gi];
+      for (int j = 8 * gi; j < 8 * gi + 8; ++j) mx = abs_maximum4(mx, xv[j]);
+      // 2^e must be a finite float: groups whose largest |x| is below
+      // 2^-112 keep e = 127 (they land below 2^15, coarser but finite)
+      const int e = min(pow2_scale_exp(quad_max_nonneg(mx)), 127);
+      sc[gi] = ldexp_f(1.0f, e);
+      if (q == 0) sexp[gi * 16 + rho] = e;
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int e = ex[j >> 3];
+      const float s = sc[j >> 3];
       const float4 v = xv[j];
-      const uint2 h = make_uint2(pack_h2(ldexp_f(v.x, e), ldexp_f(v.y, e)),
-                                 pack_h2(ldexp_f(v.z, e), ldexp_f(v.w, e)));
+      const uint2 h = make_uint2(scale_pack_h2(v.x, v.y, s), scale_pack_h2(v.z, v.w, s));
       const int frag = (j >> 3) * 4 + ((j >> 1) & 3);
       *(uint2*)(sx + frag * 1024 + (j & 1) * 512 + wr_base) = h;
     }
@@ -610,7 +627,7 @@ template <int QT>
 hipError_t launch_typed(const SkinnyArgs& a, int tiles, hipStream_t stream) {
   if (uses_x32(a.m, a.k)) {
     const unsigned grid = (unsigned)(a.nt * a.splits);
-    skinny_x32_kernel<QT, 1, true><<<grid, kThreads, 0, stream>>>(a);
+    skinny_x32_kernel<QT, 1><<<grid, kThreads, 0, stream>>>(a);
     return hipGetLastError();
   }
   switch (tiles) {
