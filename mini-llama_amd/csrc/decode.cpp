@@ -43,6 +43,8 @@ struct DecodeBuffers {
   float* x;     // residual stream [dim]
   float* x2;    // residual after attention [dim]
   float* h;     // normalised activations [dim]
+  float* xn;    // pre-scaled RMSNorm input of the next Linear: x * norm [dim]
+  float* ssq;   // its partial sums of x^2, one per 16 elements [kSsqPartsMax]
   float* qkv;   // q | k | v
   float* attn;  // attention output [n_heads * hd]
   float* ffn;   // silu(gate) * up [hidden]
@@ -119,6 +121,8 @@ int plan(const mlq_model* m, char* base, DecodeBuffers* b) {
   b->x = take(dim);
   b->x2 = take(dim);
   b->h = take(dim);
+  b->xn = take(dim);
+  b->ssq = take(kSsqPartsMax);
   b->qkv = take((size_t)qd + 2 * kvd);
   b->attn = take(qd);
   b->ffn = take(hid);
@@ -415,6 +419,48 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     return linear(w, b.h, y, bias, act);
   };
 
+  // Pre-scaled RMSNorm inputs: when every Linear of the step runs on the
+  // decode GEMV, the producer of each residual-stream vector (the
+  // embedding, the o and down projections) also writes x * next_norm and one
+  // sum of x^2 per 16 elements, so the GEMVs that consume rmsNorm(x) read a
+  // single vector and add those parts (no norm weight beside x in every
+  // workgroup).
+  const int parts = (dim + 15) / 16;
+  auto gemv_pre = [&](const mlq_weight& w) {
+    return w.type != MLQ_F32 && w.k <= gemv_max_k(w.type, 1) && gemv_prenorm_supported(w);
+  };
+  bool prenorm = parts <= kSsqPartsMax && gemv_pre(m->lm_head);
+  for (int li = 0; li < m->n_layers && prenorm; ++li) {
+    const mlq_layer& l = m->layers[li];
+    prenorm = gemv_pre(l.wq) && gemv_pre(l.wo) && gemv_pre(l.w_gate) && gemv_pre(l.w_down) &&
+              (qkv_fused(l) || (gemv_pre(l.wk) && gemv_pre(l.wv))) &&
+              (glu_fused(l) || gemv_pre(l.w_up));
+  }
+  // Linear of rmsNorm(x, norm) from the pre-scaled input b.xn / b.ssq
+  auto pre_linear = [&](const mlq_weight& w, float* y, const float* bias, int act) {
+    Epilogue e;
+    e.bias = bias;
+    e.act = act == MLQ_EPI_SWIGLU ? kEpiSwiGLU : kEpiNone;
+    e.ssq_parts = b.ssq;
+    e.ssq_count = parts;
+    e.norm_eps = m->rms_norm_eps;
+    return hip(launch_gemv(w, b.xn, y, 1, s, e));
+  };
+  // y = residual + w . x, and the pre-scaled input rmsNorm(y, next_norm)
+  auto produce = [&](const mlq_weight& w, const float* x, float* y, const float* residual,
+                     const float* next_norm) {
+    Epilogue e;
+    e.bias = residual;
+    e.next_norm = next_norm;
+    e.next_x = b.xn;
+    e.next_ssq = b.ssq;
+    return hip(launch_gemv(w, x, y, 1, s, e));
+  };
+  auto any_norm_linear = [&](const mlq_weight& w, const float* x, const float* norm, float* y,
+                             const float* bias, int act) {
+    return prenorm ? pre_linear(w, y, bias, act) : norm_linear(w, x, norm, y, bias, act);
+  };
+
   // RoPE and the cache write ride in the attention kernel where it can take
   // them (register kernel: head_dim 64 / 128 / 256, 16-byte aligned cache);
   // the embedding launch then also writes the step's RoPE table.
@@ -428,22 +474,29 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     rt.hd = hd;
     rt.theta = m->rope_theta;
   }
+  NormInput ni;
+  if (prenorm) {
+    ni.norm = m->layers[0].attn_norm;
+    ni.xn = b.xn;
+    ni.parts = b.ssq;
+  }
   if ((rc = hip(launch_embedding(m->token_embedding, m->vocab_size, dim, token_dev, token,
-                                 b.x, s, rt))) != MLQ_OK)
+                                 b.x, s, rt, ni))) != MLQ_OK)
     return rc;
   for (int li = 0; li < m->n_layers; ++li) {
     const mlq_layer& l = m->layers[li];
     // attention sublayer (forwardLayerDevice, src/forward.cc:607-640)
     if (qkv_fused(l)) {
-      if ((rc = norm_linear(l.wq, b.x, l.attn_norm, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK)
+      if ((rc = any_norm_linear(l.wq, b.x, l.attn_norm, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK)
         return rc;
     } else {
-      if ((rc = norm_linear(l.wq, b.x, l.attn_norm, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK)
+      if ((rc = any_norm_linear(l.wq, b.x, l.attn_norm, b.qkv, l.bq, MLQ_EPI_NONE)) != MLQ_OK)
         return rc;
-      if ((rc = norm_linear(l.wk, b.x, l.attn_norm, b.qkv + qd, l.bk, MLQ_EPI_NONE)) != MLQ_OK)
-        return rc;
-      if ((rc = norm_linear(l.wv, b.x, l.attn_norm, b.qkv + qd + kvd, l.bv, MLQ_EPI_NONE)) !=
+      if ((rc = any_norm_linear(l.wk, b.x, l.attn_norm, b.qkv + qd, l.bk, MLQ_EPI_NONE)) !=
           MLQ_OK)
+        return rc;
+      if ((rc = any_norm_linear(l.wv, b.x, l.attn_norm, b.qkv + qd + kvd, l.bv,
+                                MLQ_EPI_NONE)) != MLQ_OK)
         return rc;
     }
     if (!fused_rope) {
@@ -490,26 +543,36 @@ int mlq_decode_token(const mlq_model* m, const mlq_kv_cache* c, int token, int p
     }
     if ((rc = hip(launch_attention(a, s))) != MLQ_OK) return rc;
     // x2 = x + wo . attn: the residual enters as the projection's bias
-    if ((rc = linear(l.wo, b.attn, b.x2, b.x, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+    if (prenorm)
+      rc = produce(l.wo, b.attn, b.x2, b.x, l.ffn_norm);
+    else
+      rc = linear(l.wo, b.attn, b.x2, b.x, MLQ_EPI_NONE);
+    if (rc != MLQ_OK) return rc;
     // FFN sublayer
     if (glu_fused(l)) {
-      if ((rc = norm_linear(l.w_gate, b.x2, l.ffn_norm, b.ffn, nullptr, MLQ_EPI_SWIGLU)) !=
+      if ((rc = any_norm_linear(l.w_gate, b.x2, l.ffn_norm, b.ffn, nullptr, MLQ_EPI_SWIGLU)) !=
           MLQ_OK)
         return rc;
     } else {
-      if ((rc = norm_linear(l.w_gate, b.x2, l.ffn_norm, b.gate, nullptr, MLQ_EPI_NONE)) !=
+      if ((rc = any_norm_linear(l.w_gate, b.x2, l.ffn_norm, b.gate, nullptr, MLQ_EPI_NONE)) !=
           MLQ_OK)
         return rc;
-      if ((rc = norm_linear(l.w_up, b.x2, l.ffn_norm, b.up, nullptr, MLQ_EPI_NONE)) != MLQ_OK)
+      if ((rc = any_norm_linear(l.w_up, b.x2, l.ffn_norm, b.up, nullptr, MLQ_EPI_NONE)) !=
+          MLQ_OK)
         return rc;
       if ((rc = hip(launch_eltwise(kEltSwiGLU, b.gate, b.up, b.ffn, m->hidden_dim, s))) != MLQ_OK)
         return rc;
     }
     // x = x2 + w_down . ffn
-    if ((rc = linear(l.w_down, b.ffn, b.x, b.x2, MLQ_EPI_NONE)) != MLQ_OK) return rc;
+    if (prenorm)
+      rc = produce(l.w_down, b.ffn, b.x, b.x2,
+                   li + 1 < m->n_layers ? m->layers[li + 1].attn_norm : m->final_norm);
+    else
+      rc = linear(l.w_down, b.ffn, b.x, b.x2, MLQ_EPI_NONE);
+    if (rc != MLQ_OK) return rc;
   }
   // computeLogitsDevice (src/forward.cc:736-745)
-  return norm_linear(m->lm_head, b.x, m->final_norm, logits, nullptr, MLQ_EPI_NONE);
+  return any_norm_linear(m->lm_head, b.x, m->final_norm, logits, nullptr, MLQ_EPI_NONE);
 }
 
 int mlq_prefill_workspace(const mlq_model* m, int n_tokens, size_t* bytes) {

@@ -19,42 +19,6 @@
 namespace mlq {
 namespace {
 
-// Reductions over the first N lanes of each 16-lane row with DPP (VALU
-// lane permutes, no LDS round trip): xor 1 and xor 2 as quad permutes, then
-// row_half_mirror (lane i <-> 7 - i: pairs the two quads of 8 lanes) and
-// row_mirror (i <-> 15 - i: pairs the two halves of the row). Every lane of
-// the N-lane group ends with the group's result.
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
-constexpr int kDppHalfMirror = 0x141;
-constexpr int kDppMirror = 0x140;
-
-template <int N>
-__device__ __forceinline__ float row_sum(float v) {
-  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32, "row_sum width");
-  v += dpp<kDppXor1>(v);
-  if constexpr (N >= 4) v += dpp<kDppXor2>(v);
-  if constexpr (N >= 8) v += dpp<kDppHalfMirror>(v);
-  if constexpr (N >= 16) v += dpp<kDppMirror>(v);
-  if constexpr (N >= 32) v += __shfl_xor(v, 16);
-  return v;
-}
-template <int N>
-__device__ __forceinline__ float row_max(float v) {
-  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32, "row_max width");
-  v = fmaxf(v, dpp<kDppXor1>(v));
-  if constexpr (N >= 4) v = fmaxf(v, dpp<kDppXor2>(v));
-  if constexpr (N >= 8) v = fmaxf(v, dpp<kDppHalfMirror>(v));
-  if constexpr (N >= 16) v = fmaxf(v, dpp<kDppMirror>(v));
-  if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16));
-  return v;
-}
-
 __device__ __forceinline__ int read_scalar(const int32_t* dev, int host) {
   return dev != nullptr ? *dev : host;
 }
@@ -188,11 +152,20 @@ __global__ __launch_bounds__(256) void embed_kernel(const float* __restrict__ ta
                                                     const int32_t* token_dev, int token,
                                                     float* __restrict__ y, float* rope_cs,
                                                     const int32_t* pos_dev, int pos, int hd,
-                                                    float theta) {
+                                                    float theta, NormInput ni) {
   const int t = read_scalar(token_dev, token);
   const bool ok = t >= 0 && t < vocab;
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x)
-    y[i] = ok ? table[(size_t)t * dim + i] : __builtin_nanf("");
+  // the grid covers dim, one element per thread (launch_embedding)
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const float v = i < dim ? (ok ? table[(size_t)t * dim + i] : __builtin_nanf("")) : 0.0f;
+  if (i < dim) y[i] = v;
+  if (ni.norm != nullptr) {
+    // the first layer's pre-scaled RMSNorm input: v * norm, and per 16
+    // elements the sum of v^2 (the decode GEMV producer's tree)
+    const float sq = row_sum<16>(v * v);
+    if (i < dim) ni.xn[i] = v * ni.norm[i];
+    if ((threadIdx.x & 15) == 0 && i < dim) ni.parts[i >> 4] = sq;
+  }
   if (rope_cs != nullptr && blockIdx.x == 0) {
     const int p = read_scalar(pos_dev, pos);
     const int half = hd >> 1;
@@ -655,10 +628,16 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
       s[g] += qv.w * kreg[i].w;
     }
   }
+  // (lanes p, p + P, p + 2P, ... hold the parts of position p: xor steps P
+  // .. 32, the ones within a row as DPP, across rows as lane swaps)
 #pragma unroll
-  for (int off = P; off < 64; off <<= 1)
+  for (int g = 0; g < GMAX; ++g) {
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) s[g] += __shfl_xor(s[g], off);
+    for (int off = P; off < 8; off <<= 1) s[g] += __shfl_xor(s[g], off);
+    if constexpr (P <= 8) s[g] += dpp<kDppRor8>(s[g]);
+    if constexpr (P <= 16) s[g] = xor16_sum(s[g]);
+    s[g] = xor32_sum(s[g]);
+  }
   // every part holds the full score now: reduce over the P positions only
   // (P lanes of a 16-lane row, or two rows when P = 32)
   const bool valid = tp < nt;
@@ -1278,10 +1257,11 @@ hipError_t launch_softmax(const float* x, float* y, int64_t n, hipStream_t strea
 }
 
 hipError_t launch_embedding(const float* table, int vocab, int dim, const int32_t* token_dev,
-                            int token, float* y, hipStream_t stream, const RopeTable& rt) {
+                            int token, float* y, hipStream_t stream, const RopeTable& rt,
+                            const NormInput& ni) {
   const int blocks = (dim + 255) / 256;
   hipLaunchKernelGGL(embed_kernel, dim3(blocks), dim3(256), 0, stream, table, vocab, dim,
-                     token_dev, token, y, rt.cs, rt.pos_dev, rt.pos, rt.hd, rt.theta);
+                     token_dev, token, y, rt.cs, rt.pos_dev, rt.pos, rt.hd, rt.theta, ni);
   return hipGetLastError();
 }
 

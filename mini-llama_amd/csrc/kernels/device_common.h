@@ -164,16 +164,80 @@ __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
 }
 
 // Sum / max over the 64 lanes of a wave (every lane gets the result).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+// ---- cross-lane reductions without LDS round trips -------------------------
+// Within a 16-lane row: DPP (xor 1 and xor 2 as quad permutes, then
+// row_half_mirror, lane i <-> 7 - i, pairing the two quads of 8 lanes, and
+// row_mirror, i <-> 15 - i, pairing the two halves). Across rows: gfx950's
+// v_permlane16_swap (rows 0 <-> 1, 2 <-> 3) and v_permlane32_swap (lanes
+// 0..31 <-> 32..63) on two copies of the value, whose two results are the
+// pair's low and high member in every lane. Every step combines the same
+// two values in every lane of a group, so all lanes end with bit-identical
+// results (a rotation would pair them in another order per lane).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+constexpr int kDppRor8 = 0x128;       // row_ror:8 = xor 8 within a row
+struct LanePair {
+  float lo, hi;
+};
+__device__ __forceinline__ LanePair xor16_pair(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return {__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+__device__ __forceinline__ LanePair xor32_pair(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return {__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const LanePair p = xor16_pair(v);
+  return p.lo + p.hi;
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const LanePair p = xor32_pair(v);
+  return p.lo + p.hi;
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const LanePair p = xor16_pair(v);
+  return fmaxf(p.lo, p.hi);
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const LanePair p = xor32_pair(v);
+  return fmaxf(p.lo, p.hi);
+}
+// Over the N-lane groups (N = 2 .. 64) of the wave; every lane of a group
+// ends with the group's result.
+template <int N>
+__device__ __forceinline__ float row_sum(float v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "row_sum width");
+  v += dpp<kDppXor1>(v);
+  if constexpr (N >= 4) v += dpp<kDppXor2>(v);
+  if constexpr (N >= 8) v += dpp<kDppHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp<kDppMirror>(v);
+  if constexpr (N >= 32) v = xor16_sum(v);
+  if constexpr (N >= 64) v = xor32_sum(v);
   return v;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+template <int N>
+__device__ __forceinline__ float row_max(float v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "row_max width");
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp<kDppXor2>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp<kDppMirror>(v));
+  if constexpr (N >= 32) v = xor16_max(v);
+  if constexpr (N >= 64) v = xor32_max(v);
   return v;
 }
+__device__ __forceinline__ float wave_sum(float v) { return row_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return row_max<64>(v); }
 
 // ---- output epilogue (Epilogue, kEpi* in launch.h) ---------------------------
 // silu in fp32 with the hardware exp (v_exp_f32 on g * log2(e)): within a

@@ -205,7 +205,23 @@ __device__ __forceinline__ float block_sum8(float v) {
 // VEC: k % 4 == 0 (activation rows in whole float4). A compile-time choice:
 // a runtime branch around the activation loads makes the compiler wait for
 // all of them before the weight loads are issued.
-template <int QT, int MR, int GW, bool RING, bool NORM, bool VEC>
+// Producer side of a pre-scaled RMSNorm input: lanes 0..15 hold the
+// tile's outputs v (0 elsewhere); writes v * next_norm to next_x and the
+// tile's sum of v^2 (a fixed tree over the 16 lanes) to next_ssq[tile].
+// Called by a whole wave.
+// g: next_norm of the lane's row (lanes 0..15).
+__device__ __forceinline__ void produce_norm_input(const GemvArgs& a, int tile, int lane,
+                                                   float v, float g) {
+  const float sq = row_sum<16>(v * v);
+  const int row = tile * kTileRows + lane;
+  if (lane < kTileRows && row < a.n) a.epi.next_x[row] = v * g;
+  if (lane == 0) a.epi.next_ssq[tile] = sq;
+}
+
+// NM: input RMSNorm mode (one activation row): 0 none, 1 folded (the norm
+// weight is loaded beside x and sum(x^2) taken from the staged values), 2
+// pre-scaled (x holds x * norm, sum(x^2) comes from the producer's parts).
+template <int QT, int MR, int GW, bool RING, int NM, bool VEC>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int M = a.m;
@@ -255,7 +271,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // values are x * weight and the lanes keep sum(x^2) of their elements.
   // (its register-held part is loaded with x: reading it at staging time
   // instead delays the first MFMA by a round trip, measured slower)
-  constexpr bool norm = NORM && MR == 1;
+  constexpr bool norm = NM == 1 && MR == 1;
+  constexpr bool pre = NM == 2 && MR == 1;
   const rsrc_t rg = make_rsrc(norm ? a.epi.norm + kbase : a.x, norm ? xbytes : 0u);
   float4 xr[XR], gr[norm ? XR : 1];
 #pragma unroll
@@ -267,6 +284,26 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       xr[i] = load_x4(rx, c < c4 ? c : 0x2000000, vec);
       if constexpr (norm) gr[i] = load_x4(rg, c < c4 ? c : 0x2000000, vec);
     }
+  }
+  // producer of a pre-scaled input: wave 0's lanes 0..15 hold the norm
+  // weight of their output row, requested now (not behind the final barrier)
+  constexpr bool can_produce = MR == 1 && NM == 0;
+  float gnext = 0.0f;
+  if (can_produce && a.epi.next_x != nullptr) {  // uniform
+    const rsrc_t rn = make_rsrc(a.epi.next_norm + (size_t)tile * kTileRows,
+                                wave == 0 ? (uint32_t)min(kTileRows, a.n - tile * kTileRows) * 4u
+                                          : 0u);
+    gnext = __builtin_bit_cast(float, buf_load4(rn, (uint32_t)(lane & 15) * 4u, 0));
+  }
+  // pre-scaled input: the producer's partial sums of x^2, requested now and
+  // added after the group loop (lane l holds parts 4l .. 4l+3; past
+  // ssq_count they read zero). Only wave 0's range is non-empty (the other
+  // waves' load moves no data); its scale reaches the workgroup via LDS.
+  float4 sp4 = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (pre) {
+    const rsrc_t rp =
+        make_rsrc(a.epi.ssq_parts, wave == 0 ? (uint32_t)a.epi.ssq_count * 4u : 0u);
+    sp4 = __builtin_bit_cast(float4, buf_load16(rp, (uint32_t)lane * 16u, 0));
   }
   float ssq = 0.0f;  // this lane's sum of x^2 (norm only)
   auto normed = [&](float4 v, float4 g) {
@@ -532,14 +569,26 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     ssq = wave_sum(ssq);
     if (a.split == 1) nscale = sqrtf(ssq / (float)a.k + a.epi.norm_eps);
   }
+  if constexpr (pre) {
+    // the parts added in one fixed order (DPP and scalar adds: short enough
+    // for every wave's tail; computed here rather than before the group
+    // loop, where it delayed the first MFMA; wave 0's value is the one used)
+    const float t = wave_sum((sp4.x + sp4.y) + (sp4.z + sp4.w));
+    nscale = sqrtf(t / (float)a.k + a.epi.norm_eps);
+  }
   if (a.split == 1) {
     const int row = tile * kTileRows + n;
-    if (norm) {
+    if (norm || pre) {
       acc0 = acc0 / nscale;
       acc1 = acc1 / nscale;
     }
     const float v0 = add_bias(a.epi, acc0, min(row, a.n - 1));
     const float v1 = add_bias(a.epi, acc1, min(row, a.n - 1));
+    if (can_produce && a.epi.next_x != nullptr) {  // one row, no activation
+      produce_norm_input(a, tile, lane, kq == 0 && row < a.n ? v0 : 0.0f, gnext);
+      if (kq == 0 && row < a.n) a.y[row] = v0;
+      return;
+    }
     if (a.epi.act == kEpiSwiGLU) {
       // the up row of lane n (< 8) sits in lane n + 8
       const float u0 = __shfl_xor(v0, 8);
@@ -561,17 +610,30 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   if (MR > 1 && r1 < M) part[(wave * M + r1) * kTileRows + n] = acc1;
   float* ssp = part + (size_t)a.split * M * kTileRows;  // per-slice sum(x^2)
   if (norm && lane == 0) ssp[wave] = ssq;
+  if (pre && wave == 0 && lane == 0) ssp[0] = nscale;
   __syncthreads();
   if constexpr (norm) {
     float t = 0.0f;
     for (int w = 0; w < a.split; ++w) t += ssp[w];
     nscale = sqrtf(t / (float)a.k + a.epi.norm_eps);
   }
+  if constexpr (pre) nscale = ssp[0];  // wave 0's
+
   auto slice_sum = [&](int r, int nn) {
     float s = 0.0f;
     for (int w = 0; w < a.split; ++w) s += part[(w * M + r) * kTileRows + nn];
-    return norm ? s / nscale : s;
+    return norm || pre ? s / nscale : s;
   };
+  if (can_produce && a.epi.next_x != nullptr) {  // one row, no activation
+    if (wave == 0) {
+      const int row = tile * kTileRows + (lane & 15);
+      const bool live = lane < kTileRows && row < a.n;
+      const float v = live ? add_bias(a.epi, slice_sum(0, lane & 15), row) : 0.0f;
+      produce_norm_input(a, tile, lane, v, gnext);
+      if (live) a.y[row] = v;
+    }
+    return;
+  }
   if (a.epi.act == kEpiSwiGLU) {
     for (int o = tid; o < M * 8; o += blockDim.x) {
       const int r = o / 8, c = o % 8;
@@ -702,25 +764,25 @@ Plan make_plan(int type, int m, const Geometry& geo) {
   return p;
 }
 
-template <int QT, int MR, int GW, bool RING, bool NORM, bool VEC>
+template <int QT, int MR, int GW, bool RING, int NM, bool VEC>
 hipError_t launch_vec(const GemvArgs& a, size_t lds, hipStream_t stream) {
   // Opt in to more than the default 64 KiB of dynamic LDS when needed.
   static size_t configured = 64 * 1024;
   if (lds > configured) {
     hipError_t e = hipFuncSetAttribute(
-        (const void*)gemv_kernel<QT, MR, GW, RING, NORM, VEC>,
+        (const void*)gemv_kernel<QT, MR, GW, RING, NM, VEC>,
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     configured = lds;
   }
-  gemv_kernel<QT, MR, GW, RING, NORM, VEC><<<a.nt, 64 * a.split, lds, stream>>>(a);
+  gemv_kernel<QT, MR, GW, RING, NM, VEC><<<a.nt, 64 * a.split, lds, stream>>>(a);
   return hipGetLastError();
 }
 
-template <int QT, int MR, int GW, bool RING, bool NORM>
+template <int QT, int MR, int GW, bool RING, int NM>
 hipError_t launch_kernel(const GemvArgs& a, size_t lds, hipStream_t stream) {
-  if ((a.k & 3) == 0) return launch_vec<QT, MR, GW, RING, NORM, true>(a, lds, stream);
-  return launch_vec<QT, MR, GW, RING, NORM, false>(a, lds, stream);
+  if ((a.k & 3) == 0) return launch_vec<QT, MR, GW, RING, NM, true>(a, lds, stream);
+  return launch_vec<QT, MR, GW, RING, NM, false>(a, lds, stream);
 }
 
 // The input-RMSNorm variant exists for one activation row, and not for the
@@ -730,14 +792,25 @@ constexpr bool norm_variant(int qt, int gw, bool ring) {
   return ring || !((qt == MLQ_Q8_0 && gw >= 9) || (qt == MLQ_Q4_1 && gw >= 6));
 }
 
+// The pre-scaled variant holds four registers more than the plain one: it
+// exists except for q4_1 at depth 7 (which would spill).
+constexpr bool prenorm_variant(int qt, int gw, bool ring) {
+  return ring || !(qt == MLQ_Q4_1 && gw >= 7);
+}
+
 template <int QT, int MR, int GW, bool RING>
 hipError_t launch_typed(const GemvArgs& a, size_t lds, hipStream_t stream) {
-  if (a.epi.norm != nullptr) {
-    if constexpr (MR == 1 && norm_variant(QT, GW, RING))
-      return launch_kernel<QT, MR, GW, RING, true>(a, lds, stream);
+  if (a.epi.ssq_parts != nullptr) {
+    if constexpr (MR == 1 && prenorm_variant(QT, GW, RING))
+      return launch_kernel<QT, MR, GW, RING, 2>(a, lds, stream);
     return hipErrorInvalidValue;
   }
-  return launch_kernel<QT, MR, GW, RING, false>(a, lds, stream);
+  if (a.epi.norm != nullptr) {
+    if constexpr (MR == 1 && norm_variant(QT, GW, RING))
+      return launch_kernel<QT, MR, GW, RING, 1>(a, lds, stream);
+    return hipErrorInvalidValue;
+  }
+  return launch_kernel<QT, MR, GW, RING, 0>(a, lds, stream);
 }
 
 template <int QT, int MR>
@@ -803,6 +876,15 @@ bool gemv_norm_supported(const mlq_weight& w) {
   return norm_variant(w.type, depth, p.ring);
 }
 
+bool gemv_prenorm_supported(const mlq_weight& w) {
+  if (w.type != MLQ_Q8_0 && w.type != MLQ_Q4_0 && w.type != MLQ_Q4_1) return false;
+  const Plan p = make_plan(w.type, 1, geometry(w.n, w.k));
+  if (p.lds > lds_limit()) return false;
+  int depth = p.depth;
+  if (!p.ring && w.type == MLQ_Q4_1) depth = std::min(depth, 7);
+  return prenorm_variant(w.type, depth, p.ring);
+}
+
 int gemv_max_k(int type, int m) {
   if (m < 1 || m > kGemvMaxRows) return 0;
   // the largest K whose default plan fits the LDS budget
@@ -820,6 +902,14 @@ hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
   const Geometry geo = geometry(w.n, w.k);
   if (m < 1 || m > kGemvMaxRows) return hipErrorInvalidValue;
   if (epi.norm != nullptr && m != 1) return hipErrorInvalidValue;
+  if (epi.ssq_parts != nullptr &&
+      (m != 1 || epi.norm != nullptr || epi.ssq_count < 1 || epi.ssq_count > kSsqPartsMax ||
+       ((uintptr_t)epi.ssq_parts & 15) != 0))
+    return hipErrorInvalidValue;
+  if (epi.next_x != nullptr && (m != 1 || epi.act != kEpiNone || epi.next_norm == nullptr ||
+                                epi.next_ssq == nullptr || epi.norm != nullptr ||
+                                epi.ssq_parts != nullptr))
+    return hipErrorInvalidValue;
   const Plan p = make_plan(w.type, m, geo);
   if (p.lds > lds_limit()) return hipErrorInvalidValue;
   GemvArgs a;

@@ -27,7 +27,22 @@ struct Epilogue {
   // (src/ops.cc:43-72) without a separate pass over x.
   const float* norm = nullptr;  // [k] or nullptr
   float norm_eps = 0.0f;
+  // Pre-scaled input RMSNorm (decode GEMV, one activation row): x already
+  // holds x * norm, and the sum of x^2 over the row is the sum of
+  // ssq_parts[0 .. ssq_count) (ssq_count <= kSsqPartsMax), added in a fixed
+  // order; the kernel divides its outputs by sqrt(sum / k + norm_eps).
+  const float* ssq_parts = nullptr;
+  int ssq_count = 0;
+  // Producer of that input (decode GEMV, one row, no activation): besides
+  // y, write y[r] * next_norm[r] to next_x[r] and, per 16-row tile t, the
+  // sum of the tile's y^2 to next_ssq[t].
+  const float* next_norm = nullptr;
+  float* next_x = nullptr;
+  float* next_ssq = nullptr;
 };
+// Most partial sums a pre-scaled RMSNorm input may carry (one float per
+// 16 elements: rows up to 4096).
+constexpr int kSsqPartsMax = 256;
 
 // Output option of the prefill GEMM reading the fp16 copy of x and of its
 // split-K reduce (launch_gemm_f16, launch_gemm_ws with a workspace that
@@ -60,6 +75,9 @@ int gemv_max_k(int type, int m);
 // epi.norm is honoured by the decode GEMV with m == 1 for the weights this
 // accepts (launch_gemv returns hipErrorInvalidValue for the others).
 bool gemv_norm_supported(const mlq_weight& w);
+// The decode GEMV (one row) runs w with a pre-scaled RMSNorm input
+// (epi.ssq_parts), resp. as the producer of one (epi.next_x).
+bool gemv_prenorm_supported(const mlq_weight& w);
 // Split override (0 = automatic); validated by the caller.
 void set_gemv_split(int split);
 
@@ -168,9 +186,18 @@ struct RopeTable {
   int pos = 0, hd = 0;
   float theta = 10000.0f;
 };
+// With norm non-null it also writes the first layer's pre-scaled RMSNorm
+// input (Epilogue::ssq_parts): xn = y * norm and per 16 elements the sum of
+// y^2 to parts.
+struct NormInput {
+  const float* norm = nullptr;
+  float* xn = nullptr;
+  float* parts = nullptr;
+};
 hipError_t launch_embedding(const float* table, int vocab, int dim, const int32_t* token_dev,
                             int token, float* y, hipStream_t stream,
-                            const RopeTable& rt = RopeTable());
+                            const RopeTable& rt = RopeTable(),
+                            const NormInput& ni = NormInput());
 // RoPE on q [n_heads][hd] and k [n_kv][hd] at position pos (pos_dev
 // overrides). With keys/values non-null the rotated k and v go to cache row
 // (layer, pos) of a [layers][max_seq][n_kv][hd] cache and k is left as is.

@@ -419,7 +419,12 @@ def test_tiny_model_greedy_generation(pkg, oracle, cuda):
                       "max_seq_len": 160}, "bias": True, "tokens": 100}, True),
     ("q4_1", {"cfg": {"dim": 512, "n_heads": 2, "n_kv_heads": 2, "rope_type": 1}}, True),
     ("q4_0", {"cfg": {"dim": 1024, "n_heads": 16, "n_kv_heads": 2, "hidden_dim": 256,
-                      "rope_type": 1, "max_seq_len": 80}}, True)])
+                      "rope_type": 1, "max_seq_len": 80}}, True),
+    # dim not a multiple of 16: the last 16-row tile of the o / down
+    # projections (producers of the next RMSNorm input) is partial
+    ("q4_0", {"cfg": {"dim": 136, "n_heads": 4, "n_kv_heads": 2, "hidden_dim": 200}}, True),
+    ("q8_0", {"cfg": {"dim": 200, "n_heads": 2, "n_kv_heads": 1, "hidden_dim": 96},
+              "bias": True}, False)])
 def test_synthetic_models_match_oracle(pkg, oracle, cuda, qtype, kw, fuse):
     import mini_llama_amd.synth as synth
     cfg = dict(vocab_size=160, dim=128, hidden_dim=256, n_layers=3, n_heads=4, n_kv_heads=2,
