@@ -12,6 +12,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <stdint.h>
 
 #include "device_common.h"
@@ -372,6 +373,9 @@ struct AttnArgs {
   float* kc;             // the cache, writable (same arrays as keys / values)
   float* vc;
   int neox;
+  // register kernel: the kv head's query heads split over hsplit workgroups
+  // of hper heads (the last may have fewer); 1 and group otherwise
+  int hsplit = 1, hper = 1;
 };
 
 // Partial arrays of query row r: m and l [n_heads][chunks], acc
@@ -549,12 +553,25 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
   const int len = pos + 1;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int tb = blockIdx.x * (W * P);  // first position of the workgroup
-  if (pos < 0 || pos >= a.pos_limit || tb >= len) return;
+  // grid x: chunks, or with a head split (hsplit > 1) chunks x splits laid
+  // out so that the splits of one chunk have workgroup ids of equal residue
+  // mod 8 (the XCD a workgroup runs on): they read the chunk's K/V rows
+  // through one L2
+  int chunk = blockIdx.x, hs = 0;
+  if (a.hsplit > 1) {
+    const int q = blockIdx.x >> 3;
+    hs = q % a.hsplit;
+    chunk = (q / a.hsplit) * 8 + (blockIdx.x & 7);
+  }
+  const int tb = chunk * (W * P);  // first position of the workgroup
+  if (chunk >= a.chunks || pos < 0 || pos >= a.pos_limit || tb >= len) return;
   const int t0 = tb + wave * P;         // first position of this wave
   const int nt = max(0, min(P, len - t0));  // 0: an idle wave past the end
+  // this workgroup takes query heads h0 .. h0 + G - 1 of the kv head's
+  // group (hper per split, the last split fewer)
   const int kvh = blockIdx.y;
-  const int G = a.group;
+  const int h0 = kvh * a.group + hs * a.hper;
+  const int G = min(a.hper, a.group - hs * a.hper);
   const int tp = lane % P;        // position of this lane in the wave's chunk
   const int part = lane / P;      // which KD dims of K
   const size_t row_stride = (size_t)a.n_kv * HD;
@@ -582,7 +599,7 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
   // below runs a fixed GMAX times with no per-head branches (their results
   // are never stored), which lets the heads' reductions interleave
   if constexpr (FUSED) {
-    const float* qraw = a.q + (size_t)qrow * a.q_stride + (size_t)kvh * G * HD;
+    const float* qraw = a.q + (size_t)qrow * a.q_stride + (size_t)h0 * HD;
     float* qf = (float*)qs;
     for (int i = threadIdx.x; i < GMAX * HD; i += W * 64) {
       const int g = i / HD;
@@ -599,7 +616,7 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
                        rope_elem<HD>(kraw, d + 3, a.neox, a.rope_cs)};
       }
     }
-    if (tb + W * P > pos) {  // the workgroup holding pos: write the cache row
+    if (hs == 0 && tb + W * P > pos) {  // the workgroup holding pos: write the cache row
       const int d = threadIdx.x;
       const size_t row = (((size_t)a.layer * a.max_seq + pos) * a.n_kv + kvh) * HD;
       if (d < HD) {
@@ -608,7 +625,7 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
       }
     }
   } else {
-    const f4_t* q4 = (const f4_t*)(a.q + (size_t)qrow * a.q_stride + (size_t)kvh * G * HD);
+    const f4_t* q4 = (const f4_t*)(a.q + (size_t)qrow * a.q_stride + (size_t)h0 * HD);
     for (int i = threadIdx.x; i < GMAX * HD / 4; i += W * 64)
       qs[i] = i < G * HD / 4 ? q4[i] : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
@@ -688,7 +705,6 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
     }
   }
   __syncthreads();
-  const int chunk = blockIdx.x;
   const Partials pp = partials_of(a, qrow);
   float* pm = pp.m;
   float* pl = pp.l;
@@ -704,7 +720,7 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
       f[w] = wm[w][g] == -INFINITY ? 0.0f : expf(wm[w][g] - mx);
       sum += wl[w][g] * f[w];
     }
-    const size_t slot = (size_t)(kvh * G + g) * a.chunks + chunk;
+    const size_t slot = (size_t)(h0 + g) * a.chunks + chunk;
     if (lane == 0) {
       pm[slot] = mx;
       pl[slot] = sum;
@@ -1353,11 +1369,12 @@ bool attention_supported(int n_heads, int n_kv, int hd) {
 template <int HD, int GMAX>
 static void attn_launch(const AttnArgs& a, hipStream_t stream) {
   if constexpr (HD != 0) {
+    const int gx = a.hsplit > 1 ? (a.chunks + 7) / 8 * 8 * a.hsplit : a.chunks;
     if (a.rope_cs != nullptr)
-      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, true>), dim3(a.chunks, a.n_kv, a.rows),
+      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, true>), dim3(gx, a.n_kv, a.rows),
                          dim3(kAttnRegWaves * 64), 0, stream, a);
     else
-      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, false>), dim3(a.chunks, a.n_kv, a.rows),
+      hipLaunchKernelGGL((attn_reg_kernel<HD, GMAX, false>), dim3(gx, a.n_kv, a.rows),
                          dim3(kAttnRegWaves * 64), 0, stream, a);
   } else {
     constexpr int CH = kAttnLdsChunk;
@@ -1370,11 +1387,22 @@ static void attn_launch(const AttnArgs& a, hipStream_t stream) {
 
 template <int HD>
 static void attn_launch_g(const AttnArgs& a, hipStream_t stream) {
-  if (a.group <= 1) attn_launch<HD, 1>(a, stream);
-  else if (a.group <= 2) attn_launch<HD, 2>(a, stream);
-  else if (a.group <= 4) attn_launch<HD, 4>(a, stream);
-  else if (a.group <= 8) attn_launch<HD, 8>(a, stream);
+  const int h = a.hper;  // query heads per workgroup
+  if (h <= 1) attn_launch<HD, 1>(a, stream);
+  else if (h <= 2) attn_launch<HD, 2>(a, stream);
+  else if (h <= 4) attn_launch<HD, 4>(a, stream);
+  else if (h <= 8) attn_launch<HD, 8>(a, stream);
   else if constexpr (HD != 64) attn_launch<HD, 16>(a, stream);
+}
+
+// Query-head split of the register kernel: MLQ_ATTN_HSPLIT (read once)
+// overrides the rule in launch_attention.
+int attn_hsplit_override() {
+  static const int v = [] {
+    const char* e = std::getenv("MLQ_ATTN_HSPLIT");
+    return e ? std::atoi(e) : 0;
+  }();
+  return v;
 }
 
 hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
@@ -1411,6 +1439,25 @@ hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   a.pos_dev = r.pos_dev;
   a.pos = r.pos;
   a.scale = sqrtf(1.0f / (float)r.hd);
+  // The register kernel is VALU-bound at decode contexts: a grid of
+  // chunks x kv heads that leaves most CUs idle runs two query heads per
+  // workgroup instead of the whole group (7 -> 2 + 2 + 2 + 1 for Qwen2-7B:
+  // 1.530 -> 1.503 ms per decode step; 4 + 3 was slower, 1 per workgroup
+  // 1.585). Long caches (chunks x kv heads > 2 x CUs) keep one workgroup per
+  // group: there the K/V reads, not the VALU, bound the kernel.
+  a.hsplit = 1;
+  a.hper = a.group;
+  if (reg) {
+    int hs = attn_hsplit_override();
+    if (hs <= 0)
+      hs = a.group >= 3 && (int64_t)a.chunks * a.n_kv <= 2 * (int64_t)device_cus()
+               ? (a.group + 1) / 2 : 1;
+    if (hs > 1) {
+      a.hsplit = std::min(hs, a.group);
+      a.hper = (a.group + a.hsplit - 1) / a.hsplit;
+      a.hsplit = (a.group + a.hper - 1) / a.hper;  // no empty split
+    }
+  }
   switch (reg ? r.hd : 0) {
     case 64: attn_launch_g<64>(a, stream); break;
     case 128: attn_launch_g<128>(a, stream); break;
