@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 #include <stdint.h>
 
 #include "device_common.h"
@@ -947,65 +948,120 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
 // the rescaled sum; the weights exp(m_c - M) go through LDS 32 chunks at a
 // time, and lanes over head dims load those 32 partials at once (predicated,
 // so one memory round trip per batch) and sum them in chunk order.
-constexpr int kCombineBatch = 32;
+// Pass 2, per (query head, query row): four waves each take 16 chunks of a
+// 64-chunk pass. The partials' addresses do not depend on the position, so
+// the first pass requests every maximum, sum and accumulator (in bounds:
+// chunks < a.chunks) together with the device position: one memory round
+// trip instead of four dependent ones. Chunks past the live range are
+// masked by selects after the loads (stale partials never enter a product).
+// Each wave rescales its chunks to its own maximum in chunk order; the four
+// waves then merge through LDS in wave order, and passes in pass order
+// (deterministic).
+constexpr int kCombineWaves = 4;
+constexpr int kCombineCpw = 16;  // chunks per wave and pass
+constexpr int kCombinePass = kCombineWaves * kCombineCpw;
 
-__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a) {
-  __shared__ float wsh[kCombineBatch];
+// KD: head dims per lane (head_dim <= 64 KD)
+template <int KD>
+__global__ __launch_bounds__(kCombineWaves * 64) void attn_combine_kernel(AttnArgs a) {
+  constexpr int kD = KD;
+  __shared__ float sm[kCombineWaves], sl[kCombineWaves];
+  __shared__ float sacc[kCombineWaves][kAttnMaxHd];
   const int qrow = blockIdx.y;
-  const int pos = read_scalar(a.pos_dev, a.pos) + qrow;
   const int head = blockIdx.x;
-  const int lane = threadIdx.x;
-  float* out = a.out + (size_t)qrow * a.out_stride + (size_t)head * a.hd;
-  if (pos < 0 || pos >= a.pos_limit) {  // only reachable through a device position
-    for (int d = lane; d < a.hd; d += 64) out[d] = __builtin_nanf("");
-    return;
-  }
-  const int chunks = (pos + a.chunk_len) / a.chunk_len;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const Partials pp = partials_of(a, qrow);
   const float* pm = pp.m + (size_t)head * a.chunks;
   const float* pl = pp.l + (size_t)head * a.chunks;
   const float* pa = pp.acc + (size_t)head * a.chunks * a.hd;
-  // global max and sum in one pass over the partials: each lane keeps a
-  // running (max, sum rescaled to it), then the lanes' pairs are merged
-  float mx = -INFINITY, ls = 0.0f;
-  for (int c = lane; c < chunks; c += 64) {
-    const float m = pm[c], l = pl[c];
-    const float nm = fmaxf(mx, m);
-    ls = (mx == -INFINITY ? 0.0f : ls * expf(mx - nm)) + (m == -INFINITY ? 0.0f : l * expf(m - nm));
-    mx = nm;
-  }
-  const float gmx = wave_max(mx);
-  const float denom = wave_sum(mx == -INFINITY ? 0.0f : ls * expf(mx - gmx));
-  mx = gmx;
-  constexpr int kD = kAttnMaxHd / 64;
-  float acc[kD];
+  float* out = a.out + (size_t)qrow * a.out_stride + (size_t)head * a.hd;
+
+  // one pass: this wave's chunks c0 + 16 wave + i; returns the wave's
+  // (max, sum, acc) rescaled to that max (m = -inf: nothing live)
+  float gm = -INFINITY, gl = 0.0f;  // running over passes (every thread)
+  float gacc[kD];
 #pragma unroll
-  for (int j = 0; j < kD; ++j) acc[j] = 0.0f;
-  for (int c0 = 0; c0 < chunks; c0 += kCombineBatch) {
-    const int nc = min(kCombineBatch, chunks - c0);
-    __syncthreads();
-    if (lane < kCombineBatch) {
-      const float m = lane < nc ? pm[c0 + lane] : -INFINITY;
-      wsh[lane] = lane < nc ? expf(m - mx) : 0.0f;
+  for (int j = 0; j < kD; ++j) gacc[j] = 0.0f;
+  int live = 0;  // live chunks (set once the position is known)
+  auto pass = [&](int c0, auto first_c) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(first_c)::value;
+    const int cw = c0 + wave * kCombineCpw;
+    float m[kCombineCpw], l[kCombineCpw], v[kCombineCpw][kD];
+#pragma unroll
+    for (int i = 0; i < kCombineCpw; ++i) {
+      const int c = min(cw + i, a.chunks - 1);  // in bounds; masked below
+      m[i] = pm[c];
+      l[i] = pl[c];
+#pragma unroll
+      for (int j = 0; j < kD; ++j) {
+        const int d = min(lane + 64 * j, a.hd - 1);
+        v[i][j] = pa[(size_t)c * a.hd + d];
+      }
     }
+    if constexpr (FIRST) {
+      const int pos = read_scalar(a.pos_dev, a.pos) + qrow;
+      live = pos < 0 || pos >= a.pos_limit ? -1 : (pos + a.chunk_len) / a.chunk_len;
+    }
+    if (live < 0) return;
+    float wmx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kCombineCpw; ++i) {
+      m[i] = cw + i < live ? m[i] : -INFINITY;
+      wmx = fmaxf(wmx, m[i]);
+    }
+    float wl = 0.0f, wacc[kD];
+#pragma unroll
+    for (int j = 0; j < kD; ++j) wacc[j] = 0.0f;
+    if (wmx != -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < kCombineCpw; ++i) {
+        const float f = m[i] == -INFINITY ? 0.0f : expf(m[i] - wmx);
+        wl += (cw + i < live ? l[i] : 0.0f) * f;
+#pragma unroll
+        for (int j = 0; j < kD; ++j) wacc[j] += (cw + i < live ? v[i][j] : 0.0f) * f;
+      }
+    }
+    // the four waves merged in wave order, then into the running result
+    __syncthreads();  // (a previous pass's readers are done with the LDS)
+    if (lane == 0) {
+      sm[wave] = wmx;
+      sl[wave] = wl;
+    }
+#pragma unroll
+    for (int j = 0; j < kD; ++j) sacc[wave][lane + 64 * j] = wacc[j];
     __syncthreads();
+    float pmx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kCombineWaves; ++w) pmx = fmaxf(pmx, sm[w]);
+    const float nm = fmaxf(gm, pmx);
+    if (nm == -INFINITY) return;  // nothing live yet (uniform)
+    const float fo = gm == -INFINITY ? 0.0f : expf(gm - nm);
+    gl *= fo;
+#pragma unroll
+    for (int j = 0; j < kD; ++j) gacc[j] *= fo;
+#pragma unroll
+    for (int w = 0; w < kCombineWaves; ++w) {
+      const float f = sm[w] == -INFINITY ? 0.0f : expf(sm[w] - nm);
+      gl += sl[w] * f;
+#pragma unroll
+      for (int j = 0; j < kD; ++j) gacc[j] += sacc[w][lane + 64 * j] * f;
+    }
+    gm = nm;
+  };
+  pass(0, std::true_type{});
+  if (live < 0) {  // only reachable through a device position
+    if (wave == 0)
+      for (int d = lane; d < a.hd; d += 64) out[d] = __builtin_nanf("");
+    return;
+  }
+  for (int c0 = kCombinePass; c0 < live; c0 += kCombinePass) pass(c0, std::false_type{});
+  if (wave == 0) {
 #pragma unroll
     for (int j = 0; j < kD; ++j) {
       const int d = lane + 64 * j;
-      if (d < a.hd) {
-        const float* col = pa + (size_t)c0 * a.hd + d;
-        float v[kCombineBatch];
-#pragma unroll
-        for (int u = 0; u < kCombineBatch; ++u) v[u] = u < nc ? col[(size_t)u * a.hd] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < kCombineBatch; ++u) acc[j] += v[u] * wsh[u];
-      }
+      if (d < a.hd) out[d] = gacc[j] / gl;
     }
-  }
-#pragma unroll
-  for (int j = 0; j < kD; ++j) {
-    const int d = lane + 64 * j;
-    if (d < a.hd) out[d] = acc[j] / denom;
   }
 }
 
@@ -1466,7 +1522,13 @@ hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(r.n_heads, a.rows), dim3(64), 0, stream, a);
+  const dim3 cgrid(r.n_heads, a.rows), cblock(kCombineWaves * 64);
+  switch ((r.hd + 63) / 64) {
+    case 1: hipLaunchKernelGGL(attn_combine_kernel<1>, cgrid, cblock, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL(attn_combine_kernel<2>, cgrid, cblock, 0, stream, a); break;
+    case 3: hipLaunchKernelGGL(attn_combine_kernel<3>, cgrid, cblock, 0, stream, a); break;
+    default: hipLaunchKernelGGL(attn_combine_kernel<4>, cgrid, cblock, 0, stream, a); break;
+  }
   return hipGetLastError();
 }
 
