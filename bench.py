@@ -52,6 +52,8 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+# seeded synthetic weights, activations and models (shared with the tests)
+sys.path.insert(1, os.path.join(ROOT, "tests"))
 import __graft_entry__ as graft  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -75,7 +77,7 @@ class Case:
     """One shape: rotated weight copies, fixed activations, output buffer."""
 
     def __init__(self, pkg, torch, qtype, m, n, k, seed, rotate=True):
-        import mini_llama_amd.synth as synth
+        from synthetic import synth
         self.pkg, self.torch = pkg, torch
         self.qtype, self.m, self.n, self.k = qtype, m, n, k
         blocks = synth.make_blocks(qtype, n, k, seed)
@@ -188,7 +190,7 @@ def bench_sweep(pkg, torch, steps, warmup, mode):
     floats instead of 2 x 18944) — no separate bias, SiLU or multiply
     launch. The weight bytes and flops are the same in every mode. Blocks are
     generated on the device and repacked there (mlq_repack_device)."""
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5000)
     xs = {kk: torch.from_numpy(synth.make_x(1, kk, 900 + kk)[0]).to("cuda")
@@ -252,7 +254,7 @@ def bench_aos(pkg, torch, qtype, m, n, k, steps, warmup, seed):
     meaning), rotated over >= 512 MB of copies: the direct AoS GEMV (m <= 8,
     no workspace) or the repack + tiled kernels."""
     import ctypes
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     blocks = synth.make_blocks(qtype, n, k, seed)
     raw = pkg.upload_aos(blocks, device="cuda")
     copies = max(1, -(-ROTATE_BYTES // raw.numel()))
@@ -374,8 +376,8 @@ def bench_gguf_load(pkg, torch, layers=4):
     device repack to the tiled layout). GB/s of GGUF bytes, page cache warm
     for both."""
     import tempfile
-    import mini_llama_amd.synth as synth
-    import mini_llama_amd.gguf_writer as gw
+    from synthetic import synth
+    from synthetic import gguf_writer as gw
     tensors = []
     for layer in range(layers):
         for i, (name, n, k) in enumerate(SWEEP_SHAPES):
@@ -435,7 +437,7 @@ def bench_decode(pkg, torch, steps, warmup, context=1024, qtype="q4_0", prefill_
     eager mlq_decode_token calls, then one HIP graph of step + greedy
     sampling replayed per token. Tokens/s and algorithmic GB/s."""
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     log(f"decode: building a {QWEN2_7B['n_layers']}-layer {qtype} model on the device")
     model = synth.synthetic_model_device(QWEN2_7B, qtype, seed=7, bias=True)
     dm = dec.DecodeModel(model)
@@ -514,7 +516,7 @@ def bench_prefill_model(pkg, torch, qtype, n, reps):
     """mlq_prefill of an n-token prompt on a Qwen2-7B-shaped model of
     another block type (the decode-step model is q4_0)."""
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     log(f"prefill: building a {QWEN2_7B['n_layers']}-layer {qtype} model on the device")
     model = synth.synthetic_model_device(QWEN2_7B, qtype, seed=9, bias=True)
     dm = dec.DecodeModel(model)
@@ -569,7 +571,7 @@ def cpu_baseline(qtype, n, k, budget_s=10.0, flavor="scalar", threads=None):
     q4_0 / q4_1 have no SIMD path there, quant.cc:637-650)."""
     oracle = graft.load_oracle()
     graft.load_package()
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     if threads is None:
         threads = cpu_threads(host_cpu())
     blocks = synth.make_blocks(qtype, n, k, 1)

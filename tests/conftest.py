@@ -44,15 +44,15 @@ def cuda():
 
 
 def make_blocks(qtype: str, n: int, k: int, seed: int) -> np.ndarray:
-    """Seeded synthetic GGUF blocks (mini-llama_amd/synth.py distributions)."""
+    """Seeded synthetic GGUF blocks (tests/synthetic/synth.py distributions)."""
     graft.load_package()
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     return synth.make_blocks(qtype, n, k, seed)
 
 
 def make_x(m: int, k: int, seed: int) -> np.ndarray:
     graft.load_package()
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     return synth.make_x(m, k, seed)
 
 

@@ -177,7 +177,7 @@ def test_manifest_loader_reads_the_tiny_model(pkg):
 
 
 def test_synthetic_model_weight_scale(pkg, oracle):
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     cfg = dict(vocab_size=64, dim=256, hidden_dim=512, n_layers=1, n_heads=4, n_kv_heads=2,
                max_seq_len=8)
     for qtype in ("q8_0", "q4_0", "q4_1", "f32"):

@@ -1,5 +1,5 @@
 """CPU: the GGUF v3 reader (mlq_gguf_*) against files written by
-mini-llama_amd/gguf_writer.py — tensor infos, data offsets and bytes exactly as
+tests/synthetic/gguf_writer.py — tensor infos, data offsets and bytes exactly as
 written, and the reference reader's acceptance rules (src/gguf.cc:398-573):
 each malformed variant is rejected with MLQ_ERR_FORMAT, each accepted
 alignment spelling accepted. No GPU calls.
@@ -13,7 +13,7 @@ import __graft_entry__ as graft
 from conftest import make_blocks
 
 graft.load_package()
-import mini_llama_amd.gguf_writer as gw  # noqa: E402
+from synthetic import gguf_writer as gw  # noqa: E402
 
 FORMAT = -7  # MLQ_ERR_FORMAT
 

@@ -426,7 +426,7 @@ def test_tiny_model_greedy_generation(pkg, oracle, cuda):
     ("q8_0", {"cfg": {"dim": 200, "n_heads": 2, "n_kv_heads": 1, "hidden_dim": 96},
               "bias": True}, False)])
 def test_synthetic_models_match_oracle(pkg, oracle, cuda, qtype, kw, fuse):
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     cfg = dict(vocab_size=160, dim=128, hidden_dim=256, n_layers=3, n_heads=4, n_kv_heads=2,
                max_seq_len=96)
     kw = dict(kw)
@@ -455,7 +455,7 @@ def test_device_built_model_matches_oracle(pkg, oracle, cuda, qtype):
     concatenation and gate|up interleave) against the oracle on the same
     bytes brought to the host."""
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     cfg = dict(vocab_size=128, dim=128, hidden_dim=192, n_layers=2, n_heads=8, n_kv_heads=2,
                max_seq_len=32, rope_type=1)
     dmodel = synth.synthetic_model_device(cfg, qtype, seed=4, bias=True)
@@ -478,7 +478,7 @@ def test_qwen2_7b_layer_at_full_size(pkg, oracle, cuda):
     """One Qwen2-7B-shaped layer (dim 3584, FFN 18944, 28 heads / 4 kv heads,
     head_dim 128, q|k|v biases) in q4_0 at BASELINE's decode shapes, stepped
     over a few positions against the oracle."""
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     cfg = dict(vocab_size=512, dim=3584, hidden_dim=18944, n_layers=1, n_heads=28,
                n_kv_heads=4, max_seq_len=64, rope_theta=1e6, rms_norm_eps=1e-6, rope_type=1)
     model = synth.synthetic_model(cfg, "q4_0", seed=5, bias=True)
@@ -491,7 +491,7 @@ def test_graph_replay_matches_eager_steps(pkg, cuda, dim, n_heads, rope_type):
     gives bitwise the logits of eager steps, with eager work in between
     (head_dim 32: separate RoPE; 128: RoPE fused into attention)."""
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     import torch
     cfg = dict(vocab_size=200, dim=dim, hidden_dim=256, n_layers=2, n_heads=n_heads,
                n_kv_heads=2, max_seq_len=80, rope_type=rope_type)
@@ -520,7 +520,7 @@ def test_device_position_out_of_range_gives_nan(pkg, cuda):
     """A device-side token or position outside the model yields NaN logits
     (no host check can see it), never an out-of-range access."""
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     cfg = dict(vocab_size=64, dim=64, hidden_dim=128, n_layers=1, n_heads=2, n_kv_heads=1,
                max_seq_len=8)
     dm = dec.DecodeModel(synth.synthetic_model(cfg, "q8_0", seed=1))
@@ -545,7 +545,7 @@ def test_device_position_past_model_in_larger_cache_gives_nan(pkg, cuda, qtype):
     writes no cache row (forwardToken rejects pos >= max_seq_len,
     src/forward.cc:42), though the cache could hold the row."""
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     # head_dim 128 (register attention kernel, fused RoPE) and 48 (LDS kernel)
     for dim, n_heads in ((256, 2), (96, 2)):
         cfg = dict(vocab_size=64, dim=dim, hidden_dim=128, n_layers=2, n_heads=n_heads,
@@ -622,7 +622,7 @@ def test_prefill_matches_sequential_oracle(pkg, oracle, cuda, qtype, kw, fuse, s
     scale per Linear, here through two layers and the residuals): 2e-3 of
     max|logit|; n <= 8 keeps the decode GEMV's fp32-class 1e-4."""
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     kw = dict(kw)
     cfg = dict(vocab_size=160, dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=2,
                max_seq_len=160)
@@ -666,7 +666,7 @@ def test_prefill_qwen2_7b_layer_at_full_size(pkg, oracle, cuda, qtype):
     workgroups per CU)."""
     import os
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     cfg = dict(vocab_size=256, dim=3584, hidden_dim=18944, n_layers=1, n_heads=28,
                n_kv_heads=4, max_seq_len=520, rope_theta=1e6, rms_norm_eps=1e-6, rope_type=1)
     model = synth.synthetic_model(cfg, qtype, seed=9, bias=True)

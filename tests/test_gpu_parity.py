@@ -490,7 +490,7 @@ def test_gguf_upload_matches_host_repack(pkg, oracle, cuda, tmp_path):
     """Tensors uploaded straight from a mapped GGUF file (device copy +
     device repack) are the same tiled bytes as the host repack of the same
     blocks, and the Linear on them meets the oracle."""
-    import mini_llama_amd.gguf_writer as gw
+    from synthetic import gguf_writer as gw
     torch = _torch()
     specs = [("blk.0.attn_q.weight", "q8_0", 40, 96), ("blk.0.ffn_up.weight", "q4_0", 33, 1024),
              ("blk.0.ffn_down.weight", "q4_1", 16, 2080)]

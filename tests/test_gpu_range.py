@@ -125,7 +125,7 @@ def test_rmsnorm_folded_gemv_range(pkg, oracle, cuda, qtype):
     """The decode step's GEMV with the input RMSNorm folded in: norm weights
     of 1e5 (normalised activations past the fp16 range) and of 1e-7."""
     import mini_llama_amd.decode as dec
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     cfg = dict(vocab_size=96, dim=256, hidden_dim=512, n_layers=1, n_heads=4, n_kv_heads=2,
                max_seq_len=16)
     for scale in (1e5, 1e-7):

@@ -240,7 +240,7 @@ def _causal_forward_f64(model, tokens):
 
 
 def _synthetic(pkg, qtype, **kw):
-    import mini_llama_amd.synth as synth
+    from synthetic import synth
     cfg = dict(vocab_size=96, dim=64, hidden_dim=96, n_layers=2, n_heads=4, n_kv_heads=2,
                max_seq_len=16)
     cfg.update(kw.pop("cfg", {}))
