@@ -325,18 +325,20 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const float* __restrict
 //    chunk in registers. L = hd/16 lanes share one position (16 dims of K
 //    each), so a wave covers P = 64/L positions (16, 8, 4) and issues every
 //    K and V load of the chunk before it uses any: one memory round trip
-//    per wave instead of one per row. Eight waves per workgroup merge their
-//    partials in LDS, so a partial covers 8P positions (128, 64, 32). The
-//    kernel is VALU-bound at decode contexts (scores and P.V of every head
-//    of the group on each lane's positions): per workgroup, 8 waves x 8
-//    positions measured 3 % faster per decode step than 4 x 16 (and 16 x 4,
-//    4 x 16 with 1 or 2 waves, 8 x 16 slower).
+//    per wave instead of one per row. Four waves per workgroup merge their
+//    partials in LDS, so a partial covers 4P positions (64, 32, 16). The
+//    kernel is VALU-bound at decode contexts (scores and P.V of the
+//    workgroup's query heads on each lane's positions), so small grids also
+//    split a kv head's query heads over several workgroups (launch_attention).
+//    Measured per decode step with that split (Qwen2-7B shape, head_dim
+//    128): 4 waves x 8 positions 1.433 ms, 8 x 8 1.452, 8 waves of 4
+//    positions (8 dims of K per lane) 1.443, 4 x 4 1.583.
 //  - any other head_dim <= 256: attn_chunk_kernel stages 32-position chunks
 //    of K, then V, through LDS.
 constexpr int kAttnMaxGroup = 16;
 constexpr int kAttnMaxHd = 256;
 constexpr int kAttnLdsChunk = 32;
-constexpr int kAttnRegWaves = 8;  // waves per workgroup of the register kernel
+constexpr int kAttnRegWaves = 4;  // waves per workgroup of the register kernel
 constexpr int kAttnRegKD = 16;    // head dims of K per lane
 __host__ __device__ constexpr bool attn_reg_hd(int hd) { return hd == 64 || hd == 128 || hd == 256; }
 // positions per workgroup: kAttnRegWaves waves of 64 * kAttnRegKD / hd positions
