@@ -946,10 +946,6 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
   }
 }
 
-// Pass 2: one wave per query head. Lanes take chunks for the global max and
-// the rescaled sum; the weights exp(m_c - M) go through LDS 32 chunks at a
-// time, and lanes over head dims load those 32 partials at once (predicated,
-// so one memory round trip per batch) and sum them in chunk order.
 // Pass 2, per (query head, query row): four waves each take 16 chunks of a
 // 64-chunk pass. The partials' addresses do not depend on the position, so
 // the first pass requests every maximum, sum and accumulator (in bounds:
