@@ -784,6 +784,16 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
   const int nchunks = kmax / KC + 1;
   const size_t row_stride = (size_t)a.n_kv * HD;
   const size_t cbase = (size_t)a.layer * a.max_seq * row_stride + (size_t)kvh * HD;
+  // K / V rows 0 .. kmax of this kv head through buffer resources (32-bit
+  // offsets, checked on the host): rows past kmax read as zeros, so no load
+  // needs a clamp (their scores are masked and their weights are zero)
+  const uint32_t rs4 = (uint32_t)row_stride * 4u;  // bytes per position
+  const uint32_t kvbytes = (uint32_t)kmax * rs4 + HD * 4u;
+  const rsrc_t rk = make_rsrc(a.keys + cbase, kvbytes);
+  const rsrc_t rv = make_rsrc(a.values + cbase, kvbytes);
+  // softmax in base 2: scores scaled by scale * log2(e), weights 2^(s - m)
+  // with the hardware exp2 (v_exp_f32)
+  const float sl2 = a.scale * 1.44269504088896341f;
   float* kw = lds + wave * SLAB;
   float* pw = kw + KC * KS;
 
@@ -817,23 +827,23 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // element f = lane + 64 u of the chunk: key f / (HD/4), float4 f % (HD/4)
+  constexpr int kKeysPerLoad = 256 / HD;  // keys covered by one 64-lane load
   auto load_k = [&](int k0, f4_t* kr) {
+    const uint32_t voff = (uint32_t)(k0 + lane / (HD / 4)) * rs4 + (uint32_t)(lane % (HD / 4)) * 16u;
 #pragma unroll
-    for (int u = 0; u < KF4; ++u) {
-      const int f = lane + 64 * u;
-      const int key = f / (HD / 4);
-      const int c4 = f - key * (HD / 4);
-      kr[u] = *(const f4_t*)(a.keys + cbase + (size_t)min(k0 + key, kmax) * row_stride + 4 * c4);
-    }
+    for (int u = 0; u < KF4; ++u)
+      kr[u] = __builtin_bit_cast(f4_t, buf_load16(rk, voff + (uint32_t)(u * kKeysPerLoad) * rs4, 0));
   };
   // B operand of P V: V[k0 + 4 st + ak][16 t + lane % 16]
   auto load_v = [&](int k0, float* vr) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int st = 0; st < 4; ++st) {
+      const uint32_t voff = (uint32_t)(k0 + 4 * st + ak) * rs4 + (uint32_t)(lane & 15) * 4u;
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
-        vr[t * 4 + st] = a.values[cbase + (size_t)min(k0 + 4 * st + ak, kmax) * row_stride +
-                                  16 * t + (lane & 15)];
+      for (int t = 0; t < NT; ++t)
+        vr[t * 4 + st] = __builtin_bit_cast(float, buf_load4(rv, voff + 64u * t, 0));
+    }
   };
   f4_t kn[KF4];
   float vn[VPRE ? NT * 4 : 1];
@@ -878,20 +888,29 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
     }
     const f4_t sacc = (sc4[0] + sc4[1]) + (sc4[2] + sc4[3]);
     const int key = k0 + (lane & 15);
-    float pr[4];
+    float pr[4], al[4];
+    bool rescale = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool ok = dvalid[i] && key <= dpos[i];
-      const float sc = ok ? sacc[i] * a.scale : -INFINITY;
+      const float sc = ok ? sacc[i] * sl2 : -INFINITY;
       const float mx = fmaxf(mrow[i], row_max<16>(sc));
       // rows with nothing visible yet keep m = -inf and weight 0
-      const float alpha = mx == -INFINITY ? 1.0f : expf(mrow[i] - mx);
-      const float p = ok ? expf(sc - mx) : 0.0f;
+      const float alpha = mx == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mrow[i] - mx);
+      const float p = ok ? __builtin_amdgcn_exp2f(sc - mx) : 0.0f;
       lrow[i] = lrow[i] * alpha + row_sum<16>(p);
       mrow[i] = mx;
       pr[i] = p;
+      al[i] = alpha;
+      rescale |= alpha != 1.0f;
+    }
+    // the accumulators (MFMA registers) are rescaled only when some row's
+    // maximum moved in this chunk (exactly 1 otherwise)
+    if (__any(rescale)) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t][i] *= alpha;
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t][i] *= al[i];
     }
     // P (D layout) -> LDS -> A layout
 #pragma unroll
@@ -937,7 +956,7 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       const float mw = mml[w * 16 + m];
-      const float f = mw == -INFINITY ? 0.0f : expf(mw - mx);
+      const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mx);
       lsum += mml[W * 16 + w * 16 + m] * f;
       o += macc[(w * 16 + m) * HD + d] * f;
     }
@@ -1570,6 +1589,8 @@ hipError_t launch_attention_prefill(const AttnLaunch& r, hipStream_t stream) {
   if (!prefill_attention_supported(r.hd, a.group) || ((uintptr_t)r.keys & 15) != 0 ||
       ((uintptr_t)r.values & 15) != 0)
     return hipErrorInvalidValue;
+  // the kernel addresses one layer's K / V rows with 32-bit byte offsets
+  if ((uint64_t)r.max_seq * r.n_kv * r.hd * 4 >= (1ull << 32)) return hipErrorInvalidValue;
   switch (r.hd) {
     case 64: prefill_launch_g<64>(a, stream); break;
     case 128: prefill_launch_g<128>(a, stream); break;
