@@ -768,8 +768,13 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
   constexpr int KS = HD + 4;    // padded LDS row of K (16-byte aligned)
   constexpr int KF4 = KC * HD / 4 / 64;  // float4 of a K chunk per lane
   constexpr bool VPRE = HD <= 128;       // V of the next chunk loaded ahead
-  constexpr int SLAB = KC * KS + 16 * 17;          // per wave: K chunk + P
-  constexpr int MERGE = W * (16 * HD + 32);        // partial acc + max / sum
+  // LDS row strides chosen so the 64 lanes of a wave hit distinct banks:
+  // P rows 4q + i (q = lane / 16) start 16 banks apart (20 floats), merge
+  // rows likewise (HD + 4)
+  constexpr int PS = 20;                           // P row stride (floats)
+  constexpr int MS = HD + 4;                       // merge row stride (floats)
+  constexpr int SLAB = KC * KS + 16 * PS;          // per wave: K chunk + P
+  constexpr int MERGE = W * (16 * MS + 32);        // partial acc + max / sum
   constexpr int LDSF = W * SLAB > MERGE ? W * SLAB : MERGE;
   __shared__ __align__(16) float lds[LDSF];
 
@@ -914,12 +919,12 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
     }
     // P (D layout) -> LDS -> A layout
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pw[(4 * (lane >> 4) + i) * 17 + (lane & 15)] = pr[i];
+    for (int i = 0; i < 4; ++i) pw[(4 * (lane >> 4) + i) * PS + (lane & 15)] = pr[i];
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
     float pa[4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) pa[st] = pw[(lane & 15) * 17 + 4 * st + ak];
+    for (int st = 0; st < 4; ++st) pa[st] = pw[(lane & 15) * PS + 4 * st + ak];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -931,13 +936,13 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
 
   // merge the W waves' partials of every row (wave order), then store
   __syncthreads();  // every wave is done with its slab: the merge area reuses it
-  float* macc = lds;                       // [W][16][HD]
-  float* mml = lds + W * 16 * HD;          // [W][16] max, then [W][16] sum
+  float* macc = lds;                       // [W][16][MS]
+  float* mml = lds + W * 16 * MS;          // [W][16] max, then [W][16] sum
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * (lane >> 4) + i;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) macc[(wave * 16 + m) * HD + 16 * t + (lane & 15)] = acc[t][i];
+    for (int t = 0; t < NT; ++t) macc[(wave * 16 + m) * MS + 16 * t + (lane & 15)] = acc[t][i];
     if ((lane & 15) == 0) {
       mml[wave * 16 + m] = mrow[i];
       mml[W * 16 + wave * 16 + m] = lrow[i];
@@ -958,7 +963,7 @@ __global__ __launch_bounds__(prefill_waves(HD) * 64) void attn_prefill_kernel(At
       const float mw = mml[w * 16 + m];
       const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mx);
       lsum += mml[W * 16 + w * 16 + m] * f;
-      o += macc[(w * 16 + m) * HD + d] * f;
+      o += macc[(w * 16 + m) * MS + d] * f;
     }
     const size_t at = (size_t)qr * a.out_stride + (size_t)(kvh * G + m % GP) * HD + d;
     a.out[at] = o / lsum;
