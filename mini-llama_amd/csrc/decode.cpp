@@ -155,6 +155,7 @@ struct PrefillBuffers {
   float* gate;      // unfused: [n][hidden] each
   float* up;
   float* apart;     // attention partials for kPrefillAttnRows rows
+  float* rope;      // [n][head_dim] RoPE angle table of the prompt's positions
   void* lin;        // Linear workspace for n rows (and 1 row)
   size_t lin_bytes;
   // n > kSkinnyMaxRows (prefill GEMM): the fp16 GEMM input written by the
@@ -212,6 +213,7 @@ int plan_prefill(const mlq_model* m, int n, char* base, PrefillBuffers* b) {
   b->apart = (float*)take(attention_workspace_bytes(m->n_heads, m->head_dim, m->max_seq_len,
                                                     std::min(n, kPrefillAttnRows)));
   b->lin_bytes = lin;
+  b->rope = (float*)take(rows * m->head_dim * f);
   b->lin = take(lin);
   const bool gemm_rows = n > kSkinnyMaxRows;
   b->xh = gemm_rows ? (_Float16*)take(rows * f16_row_stride(dim) * 2) : nullptr;
@@ -632,6 +634,9 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
     return rc;
   if ((rc = hip(launch_embedding_rows(m->token_embedding, dim, b.tokens, n, b.x, s))) != MLQ_OK)
     return rc;
+  // the prompt's RoPE angles, once for every layer
+  if ((rc = hip(launch_rope_table(b.rope, n, start_pos, hd, m->rope_theta, s))) != MLQ_OK)
+    return rc;
   for (int li = 0; li < m->n_layers; ++li) {
     const mlq_layer& l = m->layers[li];
     RopeRows rr;
@@ -676,6 +681,7 @@ int mlq_prefill(const mlq_model* m, const mlq_kv_cache* c, const int32_t* tokens
     rr.max_seq = c->max_seq_len;
     rr.pos0 = start_pos;
     rr.theta = m->rope_theta;
+    rr.cs = b.rope;
     if ((rc = hip(launch_rope_rows(rr, s))) != MLQ_OK) return rc;
     // causal attention: query row r sees cache positions 0..start_pos + r;
     // MFMA tiles of query rows where the head dims allow, else the decode

@@ -260,7 +260,27 @@ struct RopeRowsArgs {
   float* values;
   int n_heads, n_kv, hd, neox, layer, max_seq, pos0;
   float theta;
+  const float* cs;  // [rows][hd] angle table, or null
 };
+
+// Angle of pair i at position pos (the one formula both RoPE row paths use).
+__device__ __forceinline__ void rope_angle(int pos, int i, int hd, float theta, float& sn,
+                                           float& c) {
+  const float freq = 1.0f / powf(theta, (float)(2 * i) / (float)hd);
+  sincosf((float)pos * freq, &sn, &c);
+}
+
+__global__ __launch_bounds__(256) void rope_table_kernel(float* cs, int rows, int pos0, int hd,
+                                                         float theta) {
+  const int half = hd >> 1;
+  const int r = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= half || r >= rows) return;
+  float sn, c;
+  rope_angle(pos0 + r, i, hd, theta, sn, c);
+  cs[(size_t)r * hd + i] = c;
+  cs[(size_t)r * hd + half + i] = sn;
+}
 
 __global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
   const int half = a.hd >> 1;
@@ -273,9 +293,13 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
   const int i = p - head * half;
   const int i0 = a.neox ? i : 2 * i;
   const int i1 = a.neox ? i + half : 2 * i + 1;
-  const float freq = 1.0f / powf(a.theta, (float)(2 * i) / (float)a.hd);
   float sn, c;
-  sincosf((float)pos * freq, &sn, &c);
+  if (a.cs != nullptr) {
+    c = a.cs[(size_t)r * a.hd + i];
+    sn = a.cs[(size_t)r * a.hd + half + i];
+  } else {
+    rope_angle(pos, i, a.hd, a.theta, sn, c);
+  }
   const bool is_q = head < a.n_heads;
   const int kh = head - a.n_heads;
   float* xr = is_q ? a.q + (size_t)r * a.q_stride + (size_t)head * a.hd
@@ -1400,9 +1424,18 @@ hipError_t launch_rope_rows(const RopeRows& rr, hipStream_t stream) {
   a.max_seq = rr.max_seq;
   a.pos0 = rr.pos0;
   a.theta = rr.theta;
+  a.cs = rr.cs;
   const int per_row = (rr.n_heads + rr.n_kv) * (rr.hd / 2);
   hipLaunchKernelGGL(rope_rows_kernel, dim3((per_row + 255) / 256, rr.rows), dim3(256), 0,
                      stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_table(float* cs, int rows, int pos0, int hd, float theta,
+                             hipStream_t stream) {
+  if (rows <= 0 || hd <= 0 || (hd & 1) != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((hd / 2 + 255) / 256, rows), dim3(256), 0, stream, cs,
+                     rows, pos0, hd, theta);
   return hipGetLastError();
 }
 

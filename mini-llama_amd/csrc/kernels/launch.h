@@ -269,8 +269,15 @@ struct RopeRows {
   float* values = nullptr;
   int n_heads = 0, n_kv = 0, hd = 0, neox = 0, layer = 0, max_seq = 0, pos0 = 0;
   float theta = 10000.0f;
+  // optional [rows][hd] table from launch_rope_table for positions pos0 ..
+  // pos0 + rows - 1 (the same values the kernel computes otherwise)
+  const float* cs = nullptr;
 };
 hipError_t launch_rope_rows(const RopeRows& rr, hipStream_t stream);
+// cs[r][i] = cos, cs[r][hd/2 + i] = sin of (pos0 + r) * theta^(-2i/hd) for
+// i < hd/2: the angles of launch_rope_rows, computed once for all layers.
+hipError_t launch_rope_table(float* cs, int rows, int pos0, int hd, float theta,
+                             hipStream_t stream);
 hipError_t launch_embedding_rows(const float* table, int dim, const int32_t* tokens, int rows,
                                  float* y, hipStream_t stream);
 hipError_t launch_attention(const AttnLaunch& r, hipStream_t stream);
