@@ -725,17 +725,22 @@ size_t wave_lds_bytes(int type, int m, int gw) {
 Plan make_plan(int type, int m, const Geometry& geo) {
   Plan p;
   const int env_split = split_override();
-  // Default split: about 32 waves per CU (keeping at least two groups per
-  // wave), and short
-  // enough slices that every group of a slice is in flight at once (no
-  // ring) when a workgroup of 16 waves allows it.
+  // Default split: about 32 waves per CU, keeping at least three groups per
+  // wave for one activation row (two for more rows: an 8-row wave carries
+  // more work per group), and short enough slices that every group of a
+  // slice is in flight at once (no ring) when a workgroup of 16 waves
+  // allows it. One-row shapes of K = 3584..4096 (14..16 groups) measured
+  // faster at four groups per wave than at two (q8_0 W[4096, 4096]
+  // 5.22 -> 5.01 us; the decode step's o and q|k|v projections), while
+  // W[4096, 4096] at M = 4 measured slower (5.2 -> 6.3 us).
+  const int min_groups = m == 1 ? 3 : 2;
   int split = 1;
   if (env_split >= 1 && env_split <= kMaxSplit && (env_split & (env_split - 1)) == 0) {
     split = env_split;
   } else {
     while (split < kMaxSplit && 2 * split <= geo.g) {
       const bool more_waves = geo.nt * split < kTargetWaves &&
-                              (geo.g + 2 * split - 1) / (2 * split) >= 2;
+                              (geo.g + 2 * split - 1) / (2 * split) >= min_groups;
       const bool shorter = (geo.g + split - 1) / split > max_depth(type, m);
       if (!more_waves && !shorter) break;
       split *= 2;

@@ -56,11 +56,12 @@ def test_cache_and_attention_validation(pkg):
     assert nbytes.value == 28 * 4096 * 4 * 128 * 4
     c = pkg.MlqKvCache(FAKE, FAKE, 2, 64, 4, 128)
     assert lib.mlq_attention_workspace(ctypes.byref(c), 28, ctypes.byref(nbytes)) == 0
-    # m, l and hd partials per (query head, chunk of 32 positions): the
-    # register kernel's workgroups cover 128 / 64 / 32 positions at head_dim
-    # 64 / 128 / 256, the LDS kernel 32
+    # m, l and hd partials per (query head, chunk): a chunk is the positions
+    # one register-kernel workgroup covers (four waves of 64 lanes x 16 fp32
+    # values / head_dim: 64 / 32 / 16 at head_dim 64 / 128 / 256), at most
+    # the LDS kernel's 32
     assert nbytes.value == 28 * 2 * (2 + 128) * 4
-    for hd, chunk in ((64, 32), (256, 32), (80, 32), (8, 32)):
+    for hd, chunk in ((64, 32), (128, 32), (256, 16), (80, 32), (8, 32)):
         ch = pkg.MlqKvCache(FAKE, FAKE, 2, 64, 4, hd)
         assert lib.mlq_attention_workspace(ctypes.byref(ch), 8, ctypes.byref(nbytes)) == 0
         assert nbytes.value == 8 * (64 // chunk) * (2 + hd) * 4
