@@ -1,5 +1,5 @@
 // Skinny GEMM for gfx950: y[m, n] = sum_k W[n, k] x[m, k] for m = 9..64
-// (batched decode, SURVEY config c3).
+// (batched decode: 9..64 tokens through one Linear at once).
 //
 // Between the decode GEMV (m <= 8) and the prefill GEMM (128-row tiles)
 // neither fits: a 128-row activation tile wastes most of its MFMA rows and,
