@@ -120,6 +120,19 @@ int mlq_repack_device(int type, const void* aos_dev, size_t block_count, int n,
 int mlq_dequantize(const mlq_weight* w, int row0, int rows, float* out,
                    mlq_stream_t stream);
 
+/* Quantize fp32 activations x [rows, row_size] (device, row-major) into
+ * q8_0 blocks out [rows][ceil(row_size/32)] (device, 34 B each, GGUF AoS):
+ * quantizeToQ80 (src/quant.cc:130-190) bit for bit on the GPU. Per block
+ * d = fp16(max|x| / 127) with the reference's fp16 rounding (first dropped
+ * bit rounds up, src/quant.cc:32-70), q = clamp(round(x / d), +-127) with
+ * round half away from zero, the partial last block zero padded, d = 0 and
+ * q = 0 when max|x| is 0. Elements with no integer quotient (NaN, or inf
+ * under an infinite scale; undefined in the reference) store -127, the x86
+ * conversion the reference compiles to. MLQ_ERR_BUFFER_TOO_SMALL when
+ * out_bytes < rows * ceil(row_size/32) * 34. Stream-ordered. */
+int mlq_quantize_act_q8_0(const float* x, int rows, int row_size, void* out,
+                          size_t out_bytes, mlq_stream_t stream);
+
 /* ---------------------------------------------------------------------- */
 /* Quantized Linear: y[m, n] = sum_k W[n, k] * x[m, k]                      */
 /* ---------------------------------------------------------------------- */

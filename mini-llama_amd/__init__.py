@@ -121,6 +121,7 @@ SIGNATURES = {
     "mlq_repack_host": ([_I, _P, _Z, _I, _I, _P, _Z], _I),
     "mlq_repack_device": ([_I, _P, _Z, _I, _I, _P, _Z, _P], _I),
     "mlq_dequantize": ([_WP, _I, _I, _P, _P], _I),
+    "mlq_quantize_act_q8_0": ([_P, _I, _I, _P, _Z, _P], _I),
     "mlq_linear": ([_WP, _P, _P, _I, _P], _I),
     "mlq_linear_aos": ([_I, _P, _Z, _I, _I, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_linear_aos_workspace": ([_I, _I, _I, _I, _P], _I),
@@ -421,6 +422,22 @@ def dequantize(w: TiledWeight, row0: int = 0, rows: int | None = None,
     _check(lib().mlq_dequantize(ctypes.byref(w.layout), row0, rows,
                                 out.data_ptr(), _stream(stream)),
            "mlq_dequantize")
+    return out
+
+
+def quantize_act_q8_0(x, stream=None):
+    """q8_0 blocks (uint8 [rows * ceil(k/32) * 34], GGUF AoS) of fp32 device
+    activations x [k] or [rows, k], as quantizeToQ80 (src/quant.cc:130-190)."""
+    import torch
+    if x.dtype != torch.float32 or not x.is_cuda:
+        raise ValueError("quantize_act_q8_0: x must be a float32 device tensor")
+    x = x.contiguous()
+    k = x.shape[-1]
+    rows = x.numel() // k if x.dim() >= 2 else 1
+    out = torch.empty(rows * ((k + 31) // 32) * 34, dtype=torch.uint8, device=x.device)
+    _check(lib().mlq_quantize_act_q8_0(x.data_ptr(), rows, k, out.data_ptr(), out.numel(),
+                                       _stream(stream)),
+           "mlq_quantize_act_q8_0")
     return out
 
 

@@ -203,6 +203,15 @@ int mlq_dequantize(const mlq_weight* w, int row0, int rows, float* out,
   return hip_status(launch_dequant(*w, row0, rows, out, (hipStream_t)stream));
 }
 
+int mlq_quantize_act_q8_0(const float* x, int rows, int row_size, void* out,
+                          size_t out_bytes, mlq_stream_t stream) {
+  if (x == nullptr || out == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (rows <= 0 || row_size <= 0) return MLQ_ERR_SHAPE;
+  const size_t need = (size_t)rows * (size_t)((row_size + 31) / 32) * 34;
+  if (out_bytes < need) return MLQ_ERR_BUFFER_TOO_SMALL;
+  return hip_status(launch_quantize_act_q8_0(x, rows, row_size, out, (hipStream_t)stream));
+}
+
 int mlq_linear_path(const mlq_weight* w, const float* x, float* y, int m,
                     int path, mlq_stream_t stream) {
   int rc = check_linear_weight(w);

@@ -64,6 +64,10 @@ hipError_t launch_dequant(const mlq_weight& w, int row0, int rows, float* out,
                           hipStream_t stream);
 hipError_t launch_bias(float* y, const float* bias, int m, int n,
                        hipStream_t stream);
+// rows x k fp32 (row-major) -> rows * ceil(k/32) q8_0 blocks (34 B each,
+// row-major) with quantizeToQ80's rules.
+hipError_t launch_quantize_act_q8_0(const float* x, int rows, int k, void* out,
+                                    hipStream_t stream);
 
 // gemv.hip: m in 1..8 rows of x.
 constexpr int kGemvMaxRows = 8;

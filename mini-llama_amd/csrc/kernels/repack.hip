@@ -5,6 +5,8 @@
 //    d*q+m, the reference's dequantizeFromQ* (src/quant.cc:192-392).
 //  - bias_kernel: y[m, :] += bias (the reference adds it on the host,
 //    src/cuda_quant.cu:229-235).
+//  - act_q8_0_kernel: fp32 rows -> q8_0 blocks with the reference's
+//    quantizeToQ80 rules (src/quant.cc:130-190), bit for bit.
 // These are off the hot path (one-time or debug); they favour clarity.
 #include <hip/hip_runtime.h>
 
@@ -169,6 +171,96 @@ hipError_t launch_bias(float* y, const float* bias, int m, int n,
   const unsigned threads = 256;
   const unsigned blocks = (unsigned)((total + threads - 1) / threads);
   bias_kernel<<<blocks, threads, 0, stream>>>(y, bias, m, n);
+  return hipGetLastError();
+}
+
+namespace {
+
+// fp32 -> fp16 bits as the reference's floatToFp16 (src/quant.cc:32-70)
+// rounds: the 23-bit mantissa is cut to 10 bits after adding one unit at
+// the first dropped bit (bit 12) when that bit is set (ties and above go up,
+// lower bits ignored), a carry out of the mantissa bumps the exponent;
+// exponents below the fp16 subnormal range give signed zero, above it (inf
+// and NaN included) signed infinity.
+__device__ __forceinline__ uint32_t fp16_bits_ref(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const uint32_t sign = (b >> 16) & 0x8000u;
+  int e = (int)((b >> 23) & 0xffu) - 112;  // exponent rebiased 127 -> 15
+  uint32_t man = b & 0x7fffffu;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    uint32_t s = (man | 0x800000u) >> (1 - e);  // implicit bit made explicit
+    s += (s & 0x1000u) << 1;
+    return sign | (s >> 13);
+  }
+  if (e >= 31) return sign | 0x7c00u;
+  man += (man & 0x1000u) << 1;
+  if (man & 0x800000u) {
+    man = 0;
+    if (++e >= 31) return sign | 0x7c00u;
+  }
+  return sign | ((uint32_t)e << 10) | (man >> 13);
+}
+
+// Sixteen lanes per 32-element block, two elements each: block g of the
+// [rows][nb] output is row g / nb, block g % nb of that row. Every store is
+// one aligned 16-bit word per lane (34-byte blocks are only 2-byte aligned;
+// lane 15 stores d, so no lane holds two adjacent words to merge).
+constexpr int kActLanes = 16;
+
+__global__ __launch_bounds__(256) void act_q8_0_kernel(const float* __restrict__ x,
+                                                       uint8_t* __restrict__ out,
+                                                       int rows, int k, int nb) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t g = t / kActLanes;
+  const int part = (int)(t % kActLanes);
+  const bool live = g < (uint64_t)rows * nb;  // lanes past the end only shuffle
+  const int row = live ? (int)(g / nb) : 0;
+  const int blk = live ? (int)(g % nb) : 0;
+  const int k0 = blk * 32 + part * 2;
+  const float* xr = x + (size_t)row * k;
+  float v[2];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    v[i] = live && k0 + i < k ? xr[k0 + i] : 0.0f;  // past the row: padding
+    amax = fmaxf(amax, fabsf(v[i]));  // a NaN never becomes the maximum
+  }
+#pragma unroll
+  for (int o = 1; o < kActLanes; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kActLanes));
+  if (!live) return;
+  uint32_t dbits = 0, qw = 0;
+  if (amax > 0.0f) {
+    dbits = fp16_bits_ref(amax / 127.0f);
+    const float ds = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
+    const float inv = ds == 0.0f ? 0.0f : 1.0f / ds;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float q = v[i] * inv;
+      // round half away from zero, clamp to +-127; a value no int holds
+      // (NaN, or inf * 0 under an infinite scale) takes the x86 conversion's
+      // INT_MIN the reference compiles to, i.e. -127 after the clamp
+      int qi = fabsf(q) < 2147483648.0f ? (int)roundf(q) : -127;
+      qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
+      if (k0 + i >= k) qi = 0;
+      qw |= ((uint32_t)qi & 0xffu) << (8 * i);
+    }
+  }
+  // block: fp16 d, then qs[32]
+  uint16_t* ob = (uint16_t*)(out + g * 34);
+  ob[1 + part] = (uint16_t)qw;
+  if (part == kActLanes - 1) ob[0] = (uint16_t)dbits;
+}
+
+}  // namespace
+
+hipError_t launch_quantize_act_q8_0(const float* x, int rows, int k, void* out,
+                                    hipStream_t stream) {
+  const int nb = (k + 31) / 32;
+  const uint64_t threads = (uint64_t)rows * nb * kActLanes;
+  const unsigned block = 256;
+  act_q8_0_kernel<<<(unsigned)((threads + block - 1) / block), block, 0, stream>>>(
+      x, (uint8_t*)out, rows, k, nb);
   return hipGetLastError();
 }
 
