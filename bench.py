@@ -22,7 +22,9 @@ single-launch ceiling the headline is compared against.
 model stepped token by token through mlq_decode_token, captured with its
 greedy sampling as one HIP graph, in tokens/s and algorithmic GB/s (weights
 + KV cache rows read per token), and its 512-token prefill; `prefill_q8_0`
-is the same prefill on a q8_0 model. `cpu_baseline` is the reference CPU
+is the same prefill on a q8_0 model. `prefill_int8` is configs[4] through
+the int8-MFMA variant (activation quantize pass + int8 GEMM, both timed;
+`vs_fp16` > 1 would mean it beats the fp16 GEMM). `cpu_baseline` is the reference CPU
 path (the oracle restatement) on the host cores, one thread per physical
 core up to the job's 16-thread CPU share, with lscpu's figures. `--all`
 adds the GGUF upload rate.
@@ -35,7 +37,9 @@ reference that scales the FETCH_SIZE / WRITE_SIZE counters to bytes;
 prefill GEMM counter summaries in profiles/ come from it), `--mode
 read-ceiling` times the read probe at every BASELINE weight size and
 `--mode sweep` the three 196-GEMV sweeps alone, `--mode skinny-floor` the
-load-only floors of the skinny GEMM's access pattern (mlq_read_probe_shared). `configs.c1_aos` /
+load-only floors of the skinny GEMM's access pattern (mlq_read_probe_shared),
+`--mode int8-ab` the fp16 prefill GEMM against the int8 variant on three
+prefill shapes. `configs.c1_aos` /
 `c0_aos` time mlq_linear_aos on raw GGUF blocks (the direct AoS GEMV).
 `roofline.traffic` is read from profiles/hbm_traffic_gemv_q4_0_c1.md (the
 summary of those counter runs) when it is present, else null.
@@ -58,6 +62,7 @@ import __graft_entry__ as graft  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+MFMA_I8_PEAK_TOPS = 5000.0
 ROTATE_BYTES = 512 << 20
 COPY_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_gemv_q4_0_c1.md")
@@ -168,6 +173,27 @@ def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed, eager=False):
     assert torch.isfinite(c.y).all().item()
     log(f"{qtype} m={m} n={n} k={k}: {out['us_per_call']:.2f} us/call, "
         f"{out['gbs']:.0f} GB/s, {out['tflops']:.1f} TFLOP/s")
+    del c
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_int8(pkg, torch, m, n, k, steps, warmup, seed):
+    """The int8-MFMA variant (mlq_linear_q8act: q8_0 activation quantize pass
+    + int8 GEMM, both inside the timed region) on q8_0 weights."""
+    log(f"int8 q8_0 m={m} n={n} k={k}: setup")
+    c = Case(pkg, torch, "q8_0", m, n, k, seed)
+    ws = torch.empty(pkg.workspace_bytes_q8act(c.weights[0], m), dtype=torch.uint8,
+                     device="cuda")
+
+    def launch(i):
+        pkg.linear_q8act(c.weights[i % len(c.weights)], c.x, c.y, workspace=ws)
+    per = time_graph(torch, launch, steps, warmup) / steps
+    out = {"qtype": "q8_0", "m": m, "n": n, "k": k, "us_per_call": per * 1e6,
+           "tops": alg_flops(m, n, k) / per / 1e12}
+    assert torch.isfinite(c.y).all().item()
+    log(f"int8 q8_0 m={m} n={n} k={k}: {out['us_per_call']:.2f} us/call, "
+        f"{out['tops']:.1f} TOPS")
     del c
     torch.cuda.empty_cache()
     return out
@@ -603,7 +629,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU leg")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--mode", choices=["full", "headline", "copy", "decode", "case",
-                                       "read-ceiling", "sweep", "skinny-floor"],
+                                       "read-ceiling", "sweep", "skinny-floor",
+                                       "int8-ab"],
                     default="full", help="headline/copy/decode/case: profiling runs")
     ap.add_argument("--case", default="q4_0,16,4096,4096",
                     help="--mode case: qtype,m,n,k of the one shape to launch")
@@ -649,6 +676,20 @@ def main():
              for mode in ("separate", "fused", "epilogue")}
         print(json.dumps({"mode": "sweep", **r}), flush=True)
         return
+    if args.mode == "int8-ab":
+        # fp16 GEMM (default prefill path) against the int8 variant, same box
+        rows = []
+        for (m, n, k) in ((512, 11008, 4096), (1024, 11008, 4096), (2048, 4096, 4096)):
+            f16 = bench_case(pkg, torch, "q8_0", m, n, k, min(args.steps, 200),
+                             min(args.warmup, 5), seed=4000)
+            i8 = bench_int8(pkg, torch, m, n, k, min(args.steps, 200), min(args.warmup, 5),
+                            seed=4000)
+            rows.append({"m": m, "n": n, "k": k, "fp16_us": round(f16["us_per_call"], 2),
+                         "int8_us": round(i8["us_per_call"], 2),
+                         "fp16_tflops": round(f16["tflops"], 1),
+                         "int8_tops": round(i8["tops"], 1)})
+        print(json.dumps({"mode": "int8-ab", "cases": rows}), flush=True)
+        return
     if args.mode == "case":
         qt, m, n, k = args.case.split(",")
         r = bench_case(pkg, torch, qt, int(m), int(n), int(k), args.steps, args.warmup,
@@ -693,6 +734,14 @@ def main():
                     "frac": round(prefill["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                     "dtype": "fp16 MFMA, fp32 accumulate"},
     }
+    pre8 = bench_int8(pkg, torch, 512, 11008, 4096, pre_steps, min(args.warmup, 5), seed=4000)
+    result["prefill_int8"] = {
+        "workload": "configs[4] int8 variant: X quantized to q8_0 (quantizeToQ80 rules) "
+                    "+ int8 MFMA GEMM with per-block fp32 fixup, both timed",
+        "us_per_call": round(pre8["us_per_call"], 2), "tops": round(pre8["tops"], 1),
+        "peak_tops": MFMA_I8_PEAK_TOPS, "frac": round(pre8["tops"] / MFMA_I8_PEAK_TOPS, 4),
+        "vs_fp16": round(prefill["us_per_call"] / pre8["us_per_call"], 3),
+        "dtype": "int8 MFMA, int32 per block, fp32 fixup"}
     try:
         dec = bench_decode(pkg, torch, min(args.steps, 200), min(args.warmup, 5), args.context)
         result["decode_step"] = {kk: (round(v, 4) if isinstance(v, float) else v)

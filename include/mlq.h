@@ -169,6 +169,22 @@ int mlq_linear_workspace(const mlq_weight* w, int m, size_t* bytes);
 int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
                   void* workspace, size_t workspace_bytes, mlq_stream_t stream);
 
+/* Int8 variant for q8_0 weights (MLQ_ERR_UNSUPPORTED otherwise): x is first
+ * quantized to q8_0 by quantizeToQ80's rules (src/quant.cc:130-190, as
+ * mlq_quantize_act_q8_0) into the workspace, then
+ * y[m, n] = sum_b dx[m,b] * dw[n,b] * sum_{k in b} qx[m,k] * qw[n,k] runs on
+ * int8 MFMA with an fp32 per-block scale fixup. The reference multiplies
+ * fp32 x (src/quant.cc:505-628, src/cuda_quant.cu:78-128); this variant adds
+ * the activation quantization error (at most d/2 = max|x in block| / 254
+ * per element), which grows like sqrt(k) against the tolerance's k: it
+ * meets the Linear's tolerance on N(0,1)-like rows from k ~ 1000 on. Needs
+ * |x| < 127 * 65504 (finite block scales); any m >= 1. Workspace: device,
+ * 256-byte aligned, at least mlq_linear_q8act_workspace(w, m) bytes (not
+ * NULL). No counterpart in the reference (no int8 kernel exists there). */
+int mlq_linear_q8act_workspace(const mlq_weight* w, int m, size_t* bytes);
+int mlq_linear_q8act(const mlq_weight* w, const float* x, float* y, int m,
+                     void* workspace, size_t workspace_bytes, mlq_stream_t stream);
+
 /* Output epilogues of mlq_linear_epi. */
 enum mlq_epilogue { MLQ_EPI_NONE = 0, MLQ_EPI_SWIGLU = 1 };
 

@@ -123,6 +123,8 @@ SIGNATURES = {
     "mlq_dequantize": ([_WP, _I, _I, _P, _P], _I),
     "mlq_quantize_act_q8_0": ([_P, _I, _I, _P, _Z, _P], _I),
     "mlq_linear": ([_WP, _P, _P, _I, _P], _I),
+    "mlq_linear_q8act_workspace": ([_WP, _I, ctypes.POINTER(_Z)], _I),
+    "mlq_linear_q8act": ([_WP, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_linear_aos": ([_I, _P, _Z, _I, _I, _P, _P, _I, _P, _Z, _P], _I),
     "mlq_linear_aos_workspace": ([_I, _I, _I, _I, _P], _I),
     "mlq_linear_path": ([_WP, _P, _P, _I, _I, _P], _I),
@@ -506,6 +508,37 @@ def linear(w: TiledWeight, x, y=None, path: int = PATH_AUTO, stream=None,
     _check(lib().mlq_linear_path(ctypes.byref(w.layout), x.data_ptr(),
                                  y.data_ptr(), m, path, _stream(stream)),
            "mlq_linear")
+    return y
+
+
+def workspace_bytes_q8act(w: TiledWeight, m: int) -> int:
+    """Device workspace mlq_linear_q8act needs for m activation rows."""
+    nbytes = ctypes.c_size_t(0)
+    _check(lib().mlq_linear_q8act_workspace(ctypes.byref(w.layout), m, ctypes.byref(nbytes)),
+           "mlq_linear_q8act_workspace")
+    return nbytes.value
+
+
+def linear_q8act(w: TiledWeight, x, y=None, stream=None, workspace=None):
+    """mlq_linear_q8act: the int8-MFMA variant for q8_0 weights (x quantized
+    to q8_0 blocks first, then an int8 contraction with per-block scales).
+    workspace: a uint8 device tensor of at least workspace_bytes_q8act bytes,
+    or None for the per-device grow-only one."""
+    import torch
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float32 device tensor")
+    m = 1 if x.dim() == 1 else x.shape[0]
+    if x.shape[-1] != w.k:
+        raise ValueError(f"in_features mismatch: x has {x.shape[-1]}, weight has {w.k}")
+    need = workspace_bytes_q8act(w, m)
+    ws = workspace if workspace is not None else _workspace(x.device, need)
+    if y is None:
+        y = torch.empty((w.n,) if x.dim() == 1 else (m, w.n), dtype=torch.float32,
+                        device=x.device)
+    _check(lib().mlq_linear_q8act(ctypes.byref(w.layout), x.data_ptr(), y.data_ptr(), m,
+                                  ws.data_ptr(), ws.numel() * ws.element_size(),
+                                  _stream(stream)),
+           "mlq_linear_q8act")
     return y
 
 

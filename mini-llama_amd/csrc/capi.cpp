@@ -290,6 +290,26 @@ int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
                         workspace_bytes, stream);
 }
 
+int mlq_linear_q8act_workspace(const mlq_weight* w, int m, size_t* bytes) {
+  if (bytes == nullptr) return MLQ_ERR_INVALID_ARG;
+  int rc = check_tiled(w);
+  if (rc != MLQ_OK) return rc;
+  if (w->type != MLQ_Q8_0) return MLQ_ERR_UNSUPPORTED;
+  if (m <= 0) return MLQ_ERR_SHAPE;
+  *bytes = gemm_i8_workspace_bytes(*w, m);
+  return MLQ_OK;
+}
+
+int mlq_linear_q8act(const mlq_weight* w, const float* x, float* y, int m,
+                     void* workspace, size_t workspace_bytes, mlq_stream_t stream) {
+  size_t need = 0;
+  int rc = mlq_linear_q8act_workspace(w, m, &need);
+  if (rc != MLQ_OK) return rc;
+  if (x == nullptr || y == nullptr || workspace == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (workspace_bytes < need) return MLQ_ERR_BUFFER_TOO_SMALL;
+  return hip_status(launch_gemm_i8(*w, x, y, m, workspace, (hipStream_t)stream));
+}
+
 int mlq_interleave_rows(const void* gate, const void* up, int rows,
                         size_t row_bytes, void* out) {
   if (gate == nullptr || up == nullptr || out == nullptr || row_bytes == 0)

@@ -69,6 +69,12 @@ hipError_t launch_bias(float* y, const float* bias, int m, int n,
 hipError_t launch_quantize_act_q8_0(const float* x, int rows, int k, void* out,
                                     hipStream_t stream);
 
+// gemm_i8.hip: q8_0 weights x q8_0-quantized activations on int8 MFMA
+// (activation quantize pass + GEMM). Workspace: gemm_i8_workspace_bytes.
+size_t gemm_i8_workspace_bytes(const mlq_weight& w, int m);
+hipError_t launch_gemm_i8(const mlq_weight& w, const float* x, float* y, int m,
+                          void* workspace, hipStream_t stream);
+
 // gemv.hip: m in 1..8 rows of x.
 constexpr int kGemvMaxRows = 8;
 // Returns hipErrorInvalidValue when the activation staging does not fit LDS.

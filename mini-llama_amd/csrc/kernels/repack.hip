@@ -10,6 +10,8 @@
 // These are off the hot path (one-time or debug); they favour clarity.
 #include <hip/hip_runtime.h>
 
+#include "act_q8.h"
+
 #include "../mlq_layout.h"
 #include "device_common.h"
 #include "launch.h"
@@ -176,38 +178,10 @@ hipError_t launch_bias(float* y, const float* bias, int m, int n,
 
 namespace {
 
-// fp32 -> fp16 bits as the reference's floatToFp16 (src/quant.cc:32-70)
-// rounds: the 23-bit mantissa is cut to 10 bits after adding one unit at
-// the first dropped bit (bit 12) when that bit is set (ties and above go up,
-// lower bits ignored), a carry out of the mantissa bumps the exponent;
-// exponents below the fp16 subnormal range give signed zero, above it (inf
-// and NaN included) signed infinity.
-__device__ __forceinline__ uint32_t fp16_bits_ref(float v) {
-  const uint32_t b = __builtin_bit_cast(uint32_t, v);
-  const uint32_t sign = (b >> 16) & 0x8000u;
-  int e = (int)((b >> 23) & 0xffu) - 112;  // exponent rebiased 127 -> 15
-  uint32_t man = b & 0x7fffffu;
-  if (e <= 0) {
-    if (e < -10) return sign;
-    uint32_t s = (man | 0x800000u) >> (1 - e);  // implicit bit made explicit
-    s += (s & 0x1000u) << 1;
-    return sign | (s >> 13);
-  }
-  if (e >= 31) return sign | 0x7c00u;
-  man += (man & 0x1000u) << 1;
-  if (man & 0x800000u) {
-    man = 0;
-    if (++e >= 31) return sign | 0x7c00u;
-  }
-  return sign | ((uint32_t)e << 10) | (man >> 13);
-}
-
-// Sixteen lanes per 32-element block, two elements each: block g of the
-// [rows][nb] output is row g / nb, block g % nb of that row. Every store is
-// one aligned 16-bit word per lane (34-byte blocks are only 2-byte aligned;
-// lane 15 stores d, so no lane holds two adjacent words to merge).
-constexpr int kActLanes = 16;
-
+// Sixteen lanes per 32-element block (kActLanes), two elements each: block
+// g of the [rows][nb] output is row g / nb, block g % nb of that row. Every
+// store is one aligned 16-bit word per lane (34-byte blocks are only 2-byte
+// aligned; lane 15 stores d, so no lane holds two adjacent words to merge).
 __global__ __launch_bounds__(256) void act_q8_0_kernel(const float* __restrict__ x,
                                                        uint8_t* __restrict__ out,
                                                        int rows, int k, int nb) {
@@ -219,37 +193,15 @@ __global__ __launch_bounds__(256) void act_q8_0_kernel(const float* __restrict__
   const int blk = live ? (int)(g % nb) : 0;
   const int k0 = blk * 32 + part * 2;
   const float* xr = x + (size_t)row * k;
-  float v[2];
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    v[i] = live && k0 + i < k ? xr[k0 + i] : 0.0f;  // past the row: padding
-    amax = fmaxf(amax, fabsf(v[i]));  // a NaN never becomes the maximum
-  }
-#pragma unroll
-  for (int o = 1; o < kActLanes; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kActLanes));
+  // past the row: padding (quantizes to code 0)
+  const float v0 = live && k0 < k ? xr[k0] : 0.0f;
+  const float v1 = live && k0 + 1 < k ? xr[k0 + 1] : 0.0f;
+  const Q8Codes c = q8_block_codes(v0, v1);
   if (!live) return;
-  uint32_t dbits = 0, qw = 0;
-  if (amax > 0.0f) {
-    dbits = fp16_bits_ref(amax / 127.0f);
-    const float ds = (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
-    const float inv = ds == 0.0f ? 0.0f : 1.0f / ds;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const float q = v[i] * inv;
-      // round half away from zero, clamp to +-127; a value no int holds
-      // (NaN, or inf * 0 under an infinite scale) takes the x86 conversion's
-      // INT_MIN the reference compiles to, i.e. -127 after the clamp
-      int qi = fabsf(q) < 2147483648.0f ? (int)roundf(q) : -127;
-      qi = qi > 127 ? 127 : (qi < -127 ? -127 : qi);
-      if (k0 + i >= k) qi = 0;
-      qw |= ((uint32_t)qi & 0xffu) << (8 * i);
-    }
-  }
   // block: fp16 d, then qs[32]
   uint16_t* ob = (uint16_t*)(out + g * 34);
-  ob[1 + part] = (uint16_t)qw;
-  if (part == kActLanes - 1) ob[0] = (uint16_t)dbits;
+  ob[1 + part] = (uint16_t)(((uint32_t)c.q0 & 0xffu) | (((uint32_t)c.q1 & 0xffu) << 8));
+  if (part == kActLanes - 1) ob[0] = (uint16_t)c.dbits;
 }
 
 }  // namespace
