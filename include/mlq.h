@@ -179,8 +179,10 @@ int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
  * per element), which grows like sqrt(k) against the tolerance's k: it
  * meets the Linear's tolerance on N(0,1)-like rows from k ~ 1000 on. Needs
  * |x| < 127 * 65504 (finite block scales); any m >= 1. Workspace: device,
- * 256-byte aligned, at least mlq_linear_q8act_workspace(w, m) bytes (not
- * NULL). No counterpart in the reference (no int8 kernel exists there). */
+ * 256-byte aligned
+ * (else MLQ_ERR_INVALID_ARG), at least mlq_linear_q8act_workspace(w, m)
+ * bytes (not NULL). No counterpart in the reference (no int8 kernel exists
+ * there). */
 int mlq_linear_q8act_workspace(const mlq_weight* w, int m, size_t* bytes);
 int mlq_linear_q8act(const mlq_weight* w, const float* x, float* y, int m,
                      void* workspace, size_t workspace_bytes, mlq_stream_t stream);

@@ -306,6 +306,7 @@ int mlq_linear_q8act(const mlq_weight* w, const float* x, float* y, int m,
   int rc = mlq_linear_q8act_workspace(w, m, &need);
   if (rc != MLQ_OK) return rc;
   if (x == nullptr || y == nullptr || workspace == nullptr) return MLQ_ERR_INVALID_ARG;
+  if (((uintptr_t)workspace & 255u) != 0) return MLQ_ERR_INVALID_ARG;
   if (workspace_bytes < need) return MLQ_ERR_BUFFER_TOO_SMALL;
   return hip_status(launch_gemm_i8(*w, x, y, m, workspace, (hipStream_t)stream));
 }

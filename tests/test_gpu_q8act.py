@@ -121,6 +121,9 @@ def test_q8act_workspace_contract(pkg, cuda):
     small = torch.empty(need - 1, dtype=torch.uint8, device=cuda)
     with pytest.raises(RuntimeError, match="BUFFER_TOO_SMALL|too small"):
         pkg.linear_q8act(tw, x, workspace=small)
+    big = torch.empty(need + 256, dtype=torch.uint8, device=cuda)
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        pkg.linear_q8act(tw, x, workspace=big[16:])  # large enough, misaligned
     tw4 = pkg.upload("q4_0", make_blocks("q4_0", n, k, seed=2), n, k, device=cuda)
     with pytest.raises(RuntimeError, match="UNSUPPORTED|unsupported"):
         pkg.workspace_bytes_q8act(tw4, m)
