@@ -280,6 +280,8 @@ hipError_t launch_gemm_i8(const mlq_weight& w, const float* x, float* y, int m,
     const unsigned block = 256;
     act_frag_kernel<<<(unsigned)((threads + block - 1) / block), block, 0, stream>>>(
         x, ws, (uint16_t*)(ws + q.scales_off), m, w.k, q.nb, q.nbp, q.g, q.mtp);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
   }
   const Geometry geo = geometry(w.n, w.k);
   I8Args a;
