@@ -567,12 +567,28 @@ SkinnyPlan skinny_plan(int type, int m, int n, int k) {
   SkinnyPlan best{1, 1};
   double best_t = 0.0;
   bool have = false;
-  // fp32 x in the kernel: x bytes doubled, one tile per workgroup
+  // fp32 x in the kernel: x bytes doubled, one tile per workgroup, or two
+  // (q4_0) when that saves a round of workgroups: at one workgroup per CU
+  // (its registers allow no second) a two-tile workgroup takes ~1.15x a
+  // one-tile one (q4_0 M = 16: 4096 x 4096 7.7 vs 8.8 us, one round
+  // either way; 4608 x 3584, 288 tiles: 13.8 us in two rounds vs 9.5 in one)
   const bool x32 = uses_x32(m, k);
+  if (x32 && g_tiles_override == 0 && g_splits_override == 0) {
+    int t = 1;
+    if (type == MLQ_Q4_0) {
+      const int r1 = (geo.nt + cus - 1) / cus, r2 = ((geo.nt + 1) / 2 + cus - 1) / cus;
+      if (1.15 * r2 < r1) t = 2;
+    }
+    return SkinnyPlan{t, 1};
+  }
   const double xb = x32 ? 4.0 : 2.0;
   for (int t : {1, 2, 4}) {
-    if (g_tiles_override > 0 && t != (x32 ? 1 : g_tiles_override)) continue;
-    if (x32 && t > 1) continue;
+    if (x32) {
+      // the fp32-x kernel: one tile, or two for q4_0 when overridden
+      if (t != (g_tiles_override == 2 && type == MLQ_Q4_0 ? 2 : 1)) continue;
+    } else if (g_tiles_override > 0 && t != g_tiles_override) {
+      continue;
+    }
     for (int sp : {1, 2, 4, 8, 0}) {
       // candidates 1, 2, 4, 8 within the group count, or the override alone
       if ((g_splits_override > 0) != (sp == 0) || sp > geo.g) continue;
@@ -626,6 +642,15 @@ hipError_t launch_t(const SkinnyArgs& a, hipStream_t stream) {
 template <int QT>
 hipError_t launch_typed(const SkinnyArgs& a, int tiles, hipStream_t stream) {
   if (uses_x32(a.m, a.k)) {
+    // two tiles per workgroup fit the registers without spilling for q4_0
+    // only (q8_0 / q4_1 lines are larger)
+    if constexpr (QT == MLQ_Q4_0) {
+      if (tiles == 2) {
+        const unsigned grid2 = (unsigned)((a.nt + 1) / 2 * a.splits);
+        skinny_x32_kernel<QT, 2><<<grid2, kThreads, 0, stream>>>(a);
+        return hipGetLastError();
+      }
+    }
     const unsigned grid = (unsigned)(a.nt * a.splits);
     skinny_x32_kernel<QT, 1><<<grid, kThreads, 0, stream>>>(a);
     return hipGetLastError();
