@@ -178,7 +178,7 @@ def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed, eager=False):
     return out
 
 
-def bench_int8(pkg, torch, m, n, k, steps, warmup, seed):
+def bench_int8(pkg, torch, m, n, k, steps, warmup, seed, eager=False):
     """The int8-MFMA variant (mlq_linear_q8act: q8_0 activation quantize pass
     + int8 GEMM, both inside the timed region) on q8_0 weights."""
     log(f"int8 q8_0 m={m} n={n} k={k}: setup")
@@ -188,7 +188,7 @@ def bench_int8(pkg, torch, m, n, k, steps, warmup, seed):
 
     def launch(i):
         pkg.linear_q8act(c.weights[i % len(c.weights)], c.x, c.y, workspace=ws)
-    per = time_graph(torch, launch, steps, warmup) / steps
+    per = (time_eager if eager else time_graph)(torch, launch, steps, warmup) / steps
     out = {"qtype": "q8_0", "m": m, "n": n, "k": k, "us_per_call": per * 1e6,
            "tops": alg_flops(m, n, k) / per / 1e12}
     assert torch.isfinite(c.y).all().item()
@@ -681,9 +681,9 @@ def main():
         rows = []
         for (m, n, k) in ((512, 11008, 4096), (1024, 11008, 4096), (2048, 4096, 4096)):
             f16 = bench_case(pkg, torch, "q8_0", m, n, k, min(args.steps, 200),
-                             min(args.warmup, 5), seed=4000)
+                             min(args.warmup, 5), seed=4000, eager=args.eager)
             i8 = bench_int8(pkg, torch, m, n, k, min(args.steps, 200), min(args.warmup, 5),
-                            seed=4000)
+                            seed=4000, eager=args.eager)
             rows.append({"m": m, "n": n, "k": k, "fp16_us": round(f16["us_per_call"], 2),
                          "int8_us": round(i8["us_per_call"], 2),
                          "fp16_tflops": round(f16["tflops"], 1),
