@@ -15,9 +15,17 @@
 //    offset per group, and anything past the wave's range (ragged K tails,
 //    the groups of a shorter last slice) reads as zero with no branches.
 //  - Order of issue: the wave's activation slice first, then the weight
-//    lines of all its groups (GW = groups per wave, a compile-time 1..8),
-//    then the fp32 -> fp16 hi/lo conversion of the activations into the
-//    wave's private LDS slice, which therefore overlaps the weight fetch.
+//    lines of its first groups (GW = groups per wave, a compile-time
+//    1..10), then the fp32 -> fp16 hi/lo conversion of the activations into
+//    the wave's private LDS slice, then the remaining weight lines. All
+//    waves start within ~0.5 us and the activation lines miss L2: issued
+//    behind every weight line of the slice they queue behind tens of MB of
+//    weight requests (measured: half the waves of the 4096 x 14336 q4_1
+//    GEMV staged x only after 5 us). Slices of 6+ groups and ring slices
+//    therefore stage x before any weight load (that shape 12.4 -> 10.2 us,
+//    3584 x 18944 q4_0 19.4 -> 15.7 us); shorter slices issue two groups
+//    first, which keeps HBM busy during the activation fetch (1-3 % faster
+//    than all groups first at 4 groups per wave, 3-8 % faster than x-first).
 //    The group loop has no data-dependent branch: a shorter last slice
 //    processes zero groups (zero scales, zero activations). Slices longer
 //    than the register budget run a ring of GW slots instead (GW chosen to
@@ -265,7 +273,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   constexpr bool vec = VEC;
   // Register-held part: MR == 1 covers 4 float4 per lane (8 groups); MR > 1
   // covers one float4 per lane of every row (2 groups). The rest, if any,
-  // is staged after the weight loads are issued.
+  // is loaded and staged in a second pass.
   constexpr int XR = MR == 1 ? kXRegs : kGemvMaxRows;
   // Input RMSNorm (one row): the norm weight is loaded beside x, the staged
   // values are x * weight and the lanes keep sum(x^2) of their elements.
@@ -314,12 +322,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     return float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
   };
 
-  // ---- weight loads: the first GW groups of the slice --------------------
+  // ---- weight loads: the slice's first kPre groups ------------------------
   // Issued group by group (not clustered by kind), so group 0 can start as
-  // soon as its own line and scales land.
+  // soon as its own line and scales land. The other groups of the first GW
+  // follow the activation staging (see the order of issue above).
   Slot<QT> ring[GW];
+  constexpr int kPre = (RING || GW >= 6) ? 0 : (GW < 2 ? GW : 2);
 #pragma unroll
-  for (int s = 0; s < GW; ++s) {
+  for (int s = 0; s < kPre; ++s) {
     load_group<QT>(rs, ring[s], s, qoff, soff);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -401,7 +411,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
         }
       }
     }
-    // the rest of long slices, after the weight loads are in flight
+    // the rest of long slices
     if (c4 > c_done) {
       // (rows unrolled: a runtime row index into ex[] would put it in
       // scratch memory)
@@ -468,6 +478,13 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       ex[r] = __builtin_amdgcn_readfirstlane(pow2_scale_exp(wave_max_nonneg(mx)));
     }
     stage(std::true_type{});
+  }
+  // ---- weight loads: the rest of the first GW groups ------------------------
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = kPre; s < GW; ++s) {
+    load_group<QT>(rs, ring[s], s, qoff, soff);
+    __builtin_amdgcn_sched_barrier(0);
   }
   // the slice is private to this wave: only LDS completion is needed
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
