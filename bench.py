@@ -16,7 +16,8 @@ holds the other BASELINE configurations (configs[0], [2] and [3] at M = 4,
 and configs[4]'s 196-GEMV decode sweep (28 Qwen2-7B layers x q,k,v,o,gate,
 up,down at M = 1) launched separately, fused (q|k|v, gate|up) and fused
 with the bias / SwiGLU epilogues; `roofline.read_ceiling` is one plain
-streaming read of the headline's weight bytes (mlq_read_probe), the
+streaming read of the headline's weight bytes (mlq_probe_read in the
+bench-only libmlq_probe.so), the
 single-launch ceiling the headline is compared against.
 `decode_step` reports whole-model decode: a Qwen2-7B-shaped q4_0
 model stepped token by token through mlq_decode_token, captured with its
@@ -37,7 +38,7 @@ reference that scales the FETCH_SIZE / WRITE_SIZE counters to bytes;
 prefill GEMM counter summaries in profiles/ come from it), `--mode
 read-ceiling` times the read probe at every BASELINE weight size and
 `--mode sweep` the three 196-GEMV sweeps alone, `--mode skinny-floor` the
-load-only floors of the skinny GEMM's access pattern (mlq_read_probe_shared),
+load-only floors of the skinny GEMM's access pattern (mlq_probe_read_shared),
 `--mode int8-ab` the fp16 prefill GEMM against the int8 variant on three
 prefill shapes. `configs.c1_aos` /
 `c0_aos` time mlq_linear_aos on raw GGUF blocks (the direct AoS GEMV).
@@ -155,6 +156,13 @@ def read_traffic():
     except OSError:
         return None
     return None
+
+
+def probe_lib():
+    """The bench-only read probes (mini-llama_amd/probe, libmlq_probe.so)."""
+    import importlib
+    graft.load_package()
+    return importlib.import_module("mini_llama_amd.probe")
 
 
 def log(msg):
@@ -320,7 +328,7 @@ READ_SIZES = [("c0 q8_0 4096x4096", "q8_0", 4096, 4096),
 
 
 def bench_read_ceiling(pkg, torch, steps, warmup, sizes=None):
-    """HBM read ceiling of ONE launch per size: mlq_read_probe (a streaming
+    """HBM read ceiling of ONE launch per size: mlq_probe_read (a streaming
     dwordx4 read, nothing else) over the tiled bytes of each BASELINE
     weight, plus 256 MiB and 1 GiB for the asymptote. Launches rotate over
     distinct regions of a pool of >= 512 MB + size (no Infinity-Cache reuse)
@@ -328,6 +336,7 @@ def bench_read_ceiling(pkg, torch, steps, warmup, sizes=None):
     sizes = READ_SIZES if sizes is None else sizes
     items = [(name, int(pkg.weight_layout(qt, n, k).bytes)) for name, qt, n, k in sizes]
     items += [("256 MiB", 256 << 20), ("1 GiB", 1 << 30)]
+    probe = probe_lib()
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
     out = {}
     for name, nbytes in items:
@@ -339,7 +348,7 @@ def bench_read_ceiling(pkg, torch, steps, warmup, sizes=None):
         views = [pool[i * stride:i * stride + nbytes] for i in range(slots)]
 
         def launch(i):
-            pkg.read_probe(views[i % slots], nbytes, sink)
+            probe.read(views[i % slots], nbytes, sink)
         n_steps = max(10, min(steps, int(4e10 // nbytes)))
         sec = time_graph(torch, launch, n_steps, warmup) / n_steps
         out[name] = {"bytes": nbytes, "us": round(sec * 1e6, 3),
@@ -365,11 +374,12 @@ SKINNY_FLOOR_CASES = [  # (name, shared bytes per workgroup, own bytes per wave)
 
 def bench_skinny_floor(pkg, torch, steps, warmup):
     """Load-only floors of the skinny GEMM's pattern at q4_0 W[4096, 4096]
-    (configs[3]): mlq_read_probe_shared with 256 workgroups of 8 waves, each
+    (configs[3]): mlq_probe_read_shared with 256 workgroups of 8 waves, each
     workgroup streaming its 36 KiB weight tile from HBM (rotated over a
     >= 512 MB pool) and/or reading the same x region (resident in L2 / the
     Infinity Cache after the first launch). Timed as one HIP graph."""
     wgs = 256
+    probe = probe_lib()
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
     shared = torch.ones(256 << 10, dtype=torch.uint8, device="cuda")
     out = {}
@@ -381,7 +391,7 @@ def bench_skinny_floor(pkg, torch, steps, warmup):
         views = [pool[i * stride:i * stride + per] for i in range(slots)]
 
         def launch(i):
-            pkg.read_probe_shared(shared, sb, views[i % slots], opw, wgs, sink)
+            probe.read_shared(shared, sb, views[i % slots], opw, wgs, sink)
         sec = time_graph(torch, launch, steps, warmup) / steps
         out[name] = {"shared_bytes": sb, "own_bytes_per_wave": opw,
                      "us": round(sec * 1e6, 3)}
@@ -789,7 +799,7 @@ def main():
         "gbs": rc[READ_SIZES[1][0]]["gbs"], "bytes": rc[READ_SIZES[1][0]]["bytes"],
         "asymptote_gbs_1gib": rc["1 GiB"]["gbs"],
         "frac_of_ceiling": round(head["gbs"] / rc[READ_SIZES[1][0]]["gbs"], 4),
-        "probe": "mlq_read_probe: streaming dwordx4 read of the same bytes, one launch"}
+        "probe": "mlq_probe_read (libmlq_probe.so): streaming dwordx4 read of the same bytes, one launch"}
     result["configs"] = extra
     if args.all:
         gl = bench_gguf_load(pkg, torch)

@@ -70,8 +70,10 @@ HipTensor hipQ41LinearDeviceInput(const HipTensor& x, const void* q4_1_device,
                                   int device_id = 0);
 
 // ---- Uploaded-weight entry (forwardLinearDevice-style callers) -------------
-// Runs the tiled fast path for a weight from uploadLinearWeight; throws for
-// F32 weights (the F32 cuBLAS Linear is not part of this backend).
+// Runs the tiled fast path for a quantized weight from uploadLinearWeight,
+// and an F32 weight through the fp32 GEMV (hipLinearDeviceInput), as
+// forwardLinearDevice sends F32 projections to cudaLinearDeviceInput
+// (src/forward.cc:206-209).
 HipTensor hipLinearUploaded(const HipTensor& x, const HipUploadedWeight& weight,
                             int device_id = 0);
 

@@ -318,26 +318,6 @@ int mlq_set_skinny_plan(int tiles, int splits);
 int mlq_linear_epi_noalloc(const mlq_weight* w, const float* x, float* y, int m,
                            const float* bias, int act, mlq_stream_t stream);
 
-/* Measurement aid, no counterpart in the reference: one streaming read of
- * `bytes` (a multiple of 16, 16-byte aligned device pointer) in one launch,
- * dwordx4 loads in 8 KiB chunks per wave, non-temporal like the GEMV's
- * weight lines; sink is one device word written only by chance. Timing it
- * at the byte count of a Linear gives the HBM read ceiling of a single
- * launch of that size (launch ramp and drain included). */
-int mlq_read_probe(const void* p, size_t bytes, uint32_t* sink, mlq_stream_t stream);
-
-/* Measurement aid, no counterpart in the reference: the skinny GEMM's
- * loads without its arithmetic. `workgroups` workgroups of 8 waves; every
- * workgroup reads all of `shared` (shared_bytes: 0, 64, 128 or 256 KiB;
- * wave w its 1/8 slice in 1 KiB loads) and each wave its own own_per_wave
- * bytes (a multiple of 16, at most 8 KiB; not both sizes 0) of `own`, at
- * own + (workgroup * 8 + wave) * own_per_wave (the caller sizes `own` for
- * that); every load is issued before any is used. 16-byte aligned device
- * pointers; MLQ_ERR_SHAPE for any other size. */
-int mlq_read_probe_shared(const void* shared, size_t shared_bytes, const void* own,
-                          size_t own_per_wave, int workgroups, uint32_t* sink,
-                          mlq_stream_t stream);
-
 /* Add bias[n] to every row of y[m, n] on the device (the reference adds the
  * bias on the host after download, src/cuda_quant.cu:229-235, 327-329). */
 int mlq_add_bias(float* y, const float* bias, int m, int n,

@@ -144,8 +144,6 @@ SIGNATURES = {
     "mlq_gguf_data": ([_P, ctypes.c_int64], _P),
     "mlq_gguf_upload": ([_P, ctypes.c_int64, _P, _Z, _WP, _P], _I),
     "mlq_add_bias": ([_P, _P, _I, _I, _P], _I),
-    "mlq_read_probe": ([_P, _Z, _P, _P], _I),
-    "mlq_read_probe_shared": ([_P, _Z, _P, _Z, _I, _P, _P], _I),
     "mlq_set_gemv_split": ([_I], _I),
     "mlq_set_gemm_split": ([_I], _I),
     "mlq_set_skinny_plan": ([_I, _I], _I),
@@ -591,22 +589,6 @@ def linear_aos(qtype: str, aos_dev, n: int, k: int, x, workspace=None,
                                 _stream(stream)),
            "mlq_linear_aos")
     return y
-
-
-def read_probe(buf, nbytes: int, sink, stream=None) -> None:
-    """mlq_read_probe: one streaming read of the first nbytes of a device
-    tensor (measurement aid)."""
-    _check(lib().mlq_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), _stream(stream)),
-           "mlq_read_probe")
-
-
-def read_probe_shared(shared, shared_bytes: int, own, own_per_wave: int, workgroups: int,
-                      sink, stream=None) -> None:
-    """mlq_read_probe_shared: the skinny GEMM's loads without its math."""
-    _check(lib().mlq_read_probe_shared(shared.data_ptr(), shared_bytes, own.data_ptr(),
-                                       own_per_wave, workgroups, sink.data_ptr(),
-                                       _stream(stream)),
-           "mlq_read_probe_shared")
 
 
 def set_gemv_split(split: int = 0) -> None:

@@ -380,27 +380,6 @@ int mlq_set_gemv_split(int split) {
   return MLQ_OK;
 }
 
-int mlq_read_probe(const void* p, size_t bytes, uint32_t* sink, mlq_stream_t stream) {
-  if (p == nullptr || sink == nullptr) return MLQ_ERR_INVALID_ARG;
-  if (bytes == 0 || bytes % 16 != 0 || ((uintptr_t)p & 15) != 0) return MLQ_ERR_SHAPE;
-  return hip_status(launch_read_probe(p, bytes, sink, (hipStream_t)stream));
-}
-
-int mlq_read_probe_shared(const void* shared, size_t shared_bytes, const void* own,
-                          size_t own_per_wave, int workgroups, uint32_t* sink,
-                          mlq_stream_t stream) {
-  if (shared == nullptr || own == nullptr || sink == nullptr) return MLQ_ERR_INVALID_ARG;
-  const bool shared_ok = shared_bytes == 0 || shared_bytes == (size_t)64 * 1024 ||
-                         shared_bytes == (size_t)128 * 1024 ||
-                         shared_bytes == (size_t)256 * 1024;
-  if (workgroups <= 0 || !shared_ok || own_per_wave % 16 != 0 || own_per_wave > 8 * 1024 ||
-      (shared_bytes == 0 && own_per_wave == 0) || ((uintptr_t)shared & 15) != 0 ||
-      ((uintptr_t)own & 15) != 0)
-    return MLQ_ERR_SHAPE;
-  return hip_status(launch_shared_probe(shared, shared_bytes, own, own_per_wave, workgroups,
-                                        sink, (hipStream_t)stream));
-}
-
 int mlq_add_bias(float* y, const float* bias, int m, int n,
                  mlq_stream_t stream) {
   if (y == nullptr || bias == nullptr) return MLQ_ERR_INVALID_ARG;

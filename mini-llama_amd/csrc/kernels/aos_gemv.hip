@@ -195,13 +195,8 @@ size_t aos_lds_limit() {
 
 template <int QT, int MR>
 hipError_t launch_mr(const AosArgs& a, size_t lds, hipStream_t stream) {
-  static size_t configured = 64 * 1024;
-  if (lds > configured) {
-    const hipError_t e = hipFuncSetAttribute((const void*)aos_gemv_kernel<QT, MR>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    configured = lds;
-  }
+  const hipError_t e = allow_dynamic_lds((const void*)aos_gemv_kernel<QT, MR>, lds);
+  if (e != hipSuccess) return e;
   const unsigned grid = (unsigned)((a.n + kAosWaves - 1) / kAosWaves);
   aos_gemv_kernel<QT, MR><<<grid, kAosThreads, lds, stream>>>(a);
   return hipGetLastError();

@@ -56,7 +56,10 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
+#include <set>
 #include <type_traits>
+#include <utility>
 
 #include "../mlq_layout.h"
 #include "device_common.h"
@@ -789,14 +792,9 @@ Plan make_plan(int type, int m, const Geometry& geo) {
 template <int QT, int MR, int GW, bool RING, int NM, bool VEC>
 hipError_t launch_vec(const GemvArgs& a, size_t lds, hipStream_t stream) {
   // Opt in to more than the default 64 KiB of dynamic LDS when needed.
-  static size_t configured = 64 * 1024;
-  if (lds > configured) {
-    hipError_t e = hipFuncSetAttribute(
-        (const void*)gemv_kernel<QT, MR, GW, RING, NM, VEC>,
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    configured = lds;
-  }
+  const hipError_t e =
+      allow_dynamic_lds((const void*)gemv_kernel<QT, MR, GW, RING, NM, VEC>, lds);
+  if (e != hipSuccess) return e;
   gemv_kernel<QT, MR, GW, RING, NM, VEC><<<a.nt, 64 * a.split, lds, stream>>>(a);
   return hipGetLastError();
 }
@@ -885,6 +883,25 @@ hipError_t launch_rows(const GemvArgs& a, const Plan& p, hipStream_t stream) {
 }
 
 }  // namespace
+
+hipError_t allow_dynamic_lds(const void* kernel, size_t lds) {
+  constexpr size_t kDefaultLds = 64 * 1024;
+  if (lds <= kDefaultLds) return hipSuccess;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  static std::mutex mu;
+  static std::set<std::pair<int, const void*>> raised;  // (device, kernel)
+  std::lock_guard<std::mutex> lock(mu);
+  if (raised.count({dev, kernel}) != 0) return hipSuccess;
+  int max_bytes = 0;
+  e = hipDeviceGetAttribute(&max_bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  if (e != hipSuccess) return e;
+  if ((size_t)max_bytes < lds) return hipErrorInvalidValue;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, max_bytes);
+  if (e == hipSuccess) raised.insert({dev, kernel});
+  return e;
+}
 
 void set_gemv_split(int split) { g_split_override = split; }
 

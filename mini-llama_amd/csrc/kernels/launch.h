@@ -57,6 +57,12 @@ struct GemmOut {
 // capi.cpp: MLQ status of a HIP result, recorded for mlq_last_hip_error.
 int record_hip(hipError_t e);
 
+// gemv.hip: lets `kernel` launch with `lds` bytes of dynamic LDS on the
+// current device (above the default 64 KiB the kernel's limit is raised to
+// the device maximum, once per device and kernel, under a lock: concurrent
+// launches from several host threads never race on the update).
+hipError_t allow_dynamic_lds(const void* kernel, size_t lds);
+
 // repack.hip
 hipError_t launch_repack(int type, const void* aos, int n, int k,
                          const mlq_weight& w, hipStream_t stream);
@@ -158,12 +164,6 @@ void set_skinny_plan(int tiles, int splits);
 bool aos_gemv_supported(int type, int m, int n, int k);
 hipError_t launch_aos_gemv(int type, const void* aos, int n, int k, const float* x, float* y,
                            int m, hipStream_t stream);
-
-// probe.hip: streaming read of `bytes` at p (sink: one device word).
-hipError_t launch_read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t stream);
-hipError_t launch_shared_probe(const void* shared, size_t shared_bytes, const void* own,
-                               size_t own_per_wave, int workgroups, uint32_t* sink,
-                               hipStream_t stream);
 
 // linear_f32.hip: fp32 W [n][k], any m (passes of up to 8 rows).
 hipError_t launch_linear_f32(const float* w, int n, int k, const float* x, float* y, int m,

@@ -1,8 +1,9 @@
-// Streaming-read probe: the time a plain read of `bytes` from HBM takes in
-// one launch, the ceiling that the GEMV rooflines are compared against
-// (mlq_read_probe, a measurement aid with no counterpart in the reference),
-// and a shared-read probe for the skinny GEMM's pattern
-// (mlq_read_probe_shared).
+// Bench-only measurement library (libmlq_probe.so, not part of libmlq.so's
+// C ABI): a streaming-read probe, the time a plain read of `bytes` from HBM
+// takes in one launch (the ceiling that the GEMV rooflines are compared
+// against), and a shared-read probe for the skinny GEMM's load pattern.
+// Neither has a counterpart in the reference; bench.py and the probe tests
+// are the only callers.
 // Each wave reads whole contiguous 8 KiB chunks (dwordx4, non-temporal like
 // the GEMV's weight lines), the grid sized to the chunk count; the data are
 // folded into one word so the loads cannot be removed, and the word is
@@ -11,8 +12,8 @@
 
 #include <stdint.h>
 
-#include "device_common.h"
-#include "launch.h"
+#include "kernels/device_common.h"
+#include "probe.h"
 
 namespace mlq {
 namespace {
@@ -126,3 +127,34 @@ hipError_t launch_read_probe(const void* p, size_t bytes, uint32_t* sink, hipStr
 }
 
 }  // namespace mlq
+
+extern "C" {
+
+int mlq_probe_read(const void* p, size_t bytes, uint32_t* sink, hipStream_t stream) {
+  if (p == nullptr || sink == nullptr) return MLQ_PROBE_ERR_ARG;
+  if (bytes == 0 || bytes % 16 != 0 || ((uintptr_t)p & 15) != 0) return MLQ_PROBE_ERR_SHAPE;
+  return mlq::launch_read_probe(p, bytes, sink, stream) == hipSuccess ? MLQ_PROBE_OK
+                                                                        : MLQ_PROBE_ERR_HIP;
+}
+
+int mlq_probe_read_shared(const void* shared, size_t shared_bytes, const void* own,
+                          size_t own_bytes, size_t own_per_wave, int workgroups,
+                          uint32_t* sink, hipStream_t stream) {
+  if (shared == nullptr || own == nullptr || sink == nullptr) return MLQ_PROBE_ERR_ARG;
+  const bool shared_ok = shared_bytes == 0 || shared_bytes == (size_t)64 * 1024 ||
+                         shared_bytes == (size_t)128 * 1024 ||
+                         shared_bytes == (size_t)256 * 1024;
+  if (workgroups <= 0 || !shared_ok || own_per_wave % 16 != 0 || own_per_wave > 8 * 1024 ||
+      (shared_bytes == 0 && own_per_wave == 0) || ((uintptr_t)shared & 15) != 0 ||
+      ((uintptr_t)own & 15) != 0)
+    return MLQ_PROBE_ERR_SHAPE;
+  // every wave reads own_per_wave bytes at own + (workgroup * 8 + wave) *
+  // own_per_wave: the caller's buffer must hold all of them
+  if ((size_t)workgroups * 8 * own_per_wave > own_bytes) return MLQ_PROBE_ERR_SHAPE;
+  return mlq::launch_shared_probe(shared, shared_bytes, own, own_per_wave, workgroups, sink,
+                                  stream) == hipSuccess
+             ? MLQ_PROBE_OK
+             : MLQ_PROBE_ERR_HIP;
+}
+
+}  // extern "C"

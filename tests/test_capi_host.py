@@ -199,35 +199,6 @@ def test_epilogue_validation_without_device(pkg):
     assert lib.mlq_linear_epi(ctypes.byref(w), None, 1, 1, None, 0, None, 0, None) == -1
 
 
-def test_read_probe_validation_without_device(pkg):
-    """mlq_read_probe (the bench's read-ceiling probe) checks its arguments
-    before any device work: NULL pointers, sizes that are zero or not a
-    multiple of 16, misaligned pointers."""
-    lib = pkg.lib()
-    assert lib.mlq_read_probe(None, 64, 256, None) == -1
-    assert lib.mlq_read_probe(256, 64, None, None) == -1
-    assert lib.mlq_read_probe(256, 0, 256, None) == -2
-    assert lib.mlq_read_probe(256, 40, 256, None) == -2
-    assert lib.mlq_read_probe(264, 64, 256, None) == -2
-
-
-def test_read_probe_shared_validation_without_device(pkg):
-    """mlq_read_probe_shared accepts 0/64/128/256 KiB shared regions and at
-    most 8 KiB per wave, 16-byte aligned, before touching a device."""
-    lib = pkg.lib()
-    ok = (256, 128 << 10, 512, 4608, 256, 1024, None)
-    assert lib.mlq_read_probe_shared(None, *ok[1:]) == -1
-    assert lib.mlq_read_probe_shared(*ok[:2], None, *ok[3:]) == -1
-    assert lib.mlq_read_probe_shared(*ok[:5], None, None) == -1
-    for sb in (100, 96 << 10, 512 << 10):
-        assert lib.mlq_read_probe_shared(256, sb, 512, 4608, 256, 1024, None) == -2
-    assert lib.mlq_read_probe_shared(256, 0, 512, 0, 256, 1024, None) == -2
-    assert lib.mlq_read_probe_shared(256, 0, 512, 8 * 1024 + 16, 256, 1024, None) == -2
-    assert lib.mlq_read_probe_shared(256, 0, 512, 40 + 1, 256, 1024, None) == -2
-    assert lib.mlq_read_probe_shared(256, 0, 512, 4608, 0, 1024, None) == -2
-    assert lib.mlq_read_probe_shared(264, 64 << 10, 512, 4608, 1, 1024, None) == -2
-
-
 def test_interleave_rows_permutation(pkg):
     """Rows 16t..16t+7 of the result are gate rows 8t..8t+7 and rows
     16t+8..16t+15 the matching up rows, for any row size."""

@@ -537,6 +537,11 @@ def test_bias_kernel(pkg, cuda):
                           np.array([1.0, -2.0, 0.5, 4.0], np.float32))
 
 
+def _probe():
+    import importlib
+    return importlib.import_module("mini_llama_amd.probe")
+
+
 def test_read_probe_runs_in_bounds(pkg, cuda):
     """The bench's read probe over whole and ragged sizes (a partial last
     8 KiB chunk, a partial last block of waves): it completes, and on data
@@ -546,7 +551,7 @@ def test_read_probe_runs_in_bounds(pkg, cuda):
     sink = torch.full((1,), 7, dtype=torch.int32, device=cuda)
     for nbytes in (16, 8192, 8192 + 48, 3 * 8192 * 4 + 16, 1 << 20):
         print(f"read probe {nbytes} B", flush=True)
-        pkg.read_probe(buf, nbytes, sink)
+        _probe().read(buf, nbytes, sink)
     torch.cuda.synchronize()
     assert int(sink.item()) == 7
 
@@ -565,7 +570,7 @@ def test_read_probe_shared_runs_in_bounds(pkg, cuda):
             if sb == 0 and opw == 0:
                 continue
             print(f"shared probe shared={sb} own/wave={opw}", flush=True)
-            pkg.read_probe_shared(shared, sb, own, opw, wgs, sink)
+            _probe().read_shared(shared, sb, own, opw, wgs, sink)
     torch.cuda.synchronize()
     assert int(sink.item()) == 7
 
