@@ -25,10 +25,16 @@ greedy sampling as one HIP graph, in tokens/s and algorithmic GB/s (weights
 + KV cache rows read per token), and its 512-token prefill; `prefill_q8_0`
 is the same prefill on a q8_0 model. `prefill_int8` is configs[4] through
 the int8-MFMA variant (activation quantize pass + int8 GEMM, both timed;
-`vs_fp16` > 1 would mean it beats the fp16 GEMM). `cpu_baseline` is the reference CPU
-path (the oracle restatement) on the host cores, one thread per physical
-core up to the job's 16-thread CPU share, with lscpu's figures. `--all`
-adds the GGUF upload rate.
+`vs_fp16` > 1 would mean it beats the fp16 GEMM). `prefill.mfma_ceiling` is a dense fp16 / bf16 GEMM
+of the same shape through torch.matmul (hipBLASLt) on the same box, the
+ceiling the quantized GEMM is compared against. `cpu_baseline` is the
+reference CPU path (the oracle restatement) on the host cores, one thread
+per physical core up to the job's 16-thread CPU share, with lscpu's
+figures; `cpu_baseline_builds` times every BASELINE workload (configs[0]
+to [4] and the decode sweep) in the scalar and the AVX2 build beside this
+run's GPU time. `configs.llc_hot` repeats c0-c3 on one weight copy
+(Infinity-Cache resident: labelled LLC-hot, not HBM). `--all` adds the
+GGUF upload rate.
 
 Profiling modes (one kernel family per run, for rocprofv3 counter passes):
 `--mode headline` launches only the headline GEMV (eagerly with `--eager`),
@@ -169,9 +175,9 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed, eager=False):
-    log(f"{qtype} m={m} n={n} k={k}: setup")
-    c = Case(pkg, torch, qtype, m, n, k, seed)
+def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed, eager=False, rotate=True):
+    log(f"{qtype} m={m} n={n} k={k}: setup{'' if rotate else ' (one weight copy)'}")
+    c = Case(pkg, torch, qtype, m, n, k, seed, rotate=rotate)
     sec = (time_eager if eager else time_graph)(torch, c.launch, steps, warmup)
     per = sec / steps
     out = {"qtype": qtype, "m": m, "n": n, "k": k, "copies": len(c.weights),
@@ -183,6 +189,33 @@ def bench_case(pkg, torch, qtype, m, n, k, steps, warmup, seed, eager=False):
         f"{out['gbs']:.0f} GB/s, {out['tflops']:.1f} TFLOP/s")
     del c
     torch.cuda.empty_cache()
+    return out
+
+
+def bench_dense_ceiling(torch, m, n, k, steps, warmup):
+    """A dense GEMM of the prefill shape on the same box: torch.matmul of
+    x [m, k] and W [n, k]^T (hipBLASLt), fp16 and bf16 operands, fp32
+    accumulate, W rotated over >= 512 MB of copies like the quantized case.
+    It has no weight decode to do, so it bounds what the matrix cores give
+    this shape through the vendor library."""
+    out = {}
+    for name, dt in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(11)
+        x = torch.randn(m, k, device="cuda", generator=g).to(dt)
+        copies = max(1, -(-ROTATE_BYTES // (n * k * 2)))
+        ws = [torch.randn(n, k, device="cuda", generator=g).to(dt) for _ in range(copies)]
+        y = torch.empty(m, n, device="cuda", dtype=dt)
+
+        def launch(i):
+            torch.matmul(x, ws[i % copies].t(), out=y)
+        per = time_graph(torch, launch, steps, warmup) / steps
+        out[name] = {"us_per_call": round(per * 1e6, 2),
+                     "tflops": round(alg_flops(m, n, k) / per / 1e12, 1),
+                     "copies": copies}
+        log(f"dense {name} {m}x{n}x{k}: {per * 1e6:.2f} us")
+        del x, ws, y
+        torch.cuda.empty_cache()
     return out
 
 
@@ -629,6 +662,94 @@ def cpu_baseline(qtype, n, k, budget_s=10.0, flavor="scalar", threads=None):
                       f"{build} build of oracle/quant_ref.c)"}
 
 
+def cpu_time(oracle, qtype, blocks, x, n, k, budget_s, flavor, threads):
+    """Seconds per call of the oracle Linear (the reference CPU path) on x
+    ([k] or [m, k]), repeated until `budget_s` or 1000 calls; a single warm
+    call longer than the budget is the sample itself."""
+    t0 = time.perf_counter()
+    oracle.linear(x, blocks, (n, k), qtype, threads=threads, flavor=flavor)
+    first = time.perf_counter() - t0
+    if first >= budget_s:
+        return first, 1
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.linear(x, blocks, (n, k), qtype, threads=threads, flavor=flavor)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 1000:
+            return el / reps, reps
+
+
+# every BASELINE workload: (config, key of its GPU result, qtype, m, n, k)
+CPU_WORKLOADS = [("configs[0]", "c0", "q8_0", 1, 4096, 4096),
+                 ("configs[1]", "headline", "q4_0", 1, 18944, 3584),
+                 ("configs[2]", "c2", "q4_1", 1, 4096, 14336),
+                 ("configs[3] M=4", "c3_m4", "q4_0", 4, 4096, 4096),
+                 ("configs[3] M=16", "c3_m16", "q4_0", 16, 4096, 4096),
+                 ("configs[3] M=64", "c3_m64", "q4_0", 64, 4096, 4096),
+                 ("configs[4] prefill", "prefill", "q8_0", 512, 11008, 4096)]
+
+
+def cpu_all_configs(result, threads, budget_s):
+    """The reference CPU path on every BASELINE workload, built both ways
+    (-O2 and -O2 -mavx2 -mfma, CMakeLists.txt:16-25, 192; only q8_0 has an
+    AVX2 loop, quant.cc:505-628, q4_0 / q4_1 run the scalar loop in both
+    builds), at `threads` threads, next to the GPU time of the same run.
+    The decode sweep is timed as one Qwen2-7B layer's seven GEMVs, x 28."""
+    oracle = graft.load_oracle()
+    graft.load_package()
+    from synthetic import synth
+    gpu_us = {"headline": result["ms_per_step"] * 1e3,
+              "prefill": result["prefill"]["us_per_call"]}
+    for key, v in result["configs"].items():
+        if "us_per_call" in v:
+            gpu_us[key] = v["us_per_call"]
+    rows = []
+    flavors = [f for f in ("scalar", "avx2") if oracle.flavor_available(f)]
+    for tag, key, qt, m, n, k in CPU_WORKLOADS:
+        blocks = synth.make_blocks(qt, n, k, 3000)
+        x = synth.make_x(m, k, 3001)
+        x = x[0] if m == 1 else x
+        for flavor in flavors:
+            log(f"cpu {tag} {flavor}")
+            per, reps = cpu_time(oracle, qt, blocks, x, n, k, budget_s, flavor, threads)
+            row = {"config": tag, "build": flavor, "qtype": qt, "m": m, "n": n, "k": k,
+                   "us_per_call": round(per * 1e6, 1), "cores": threads,
+                   "sample": f"{reps} call(s) of x[{m},{k}] . W[{n},{k}]^T"}
+            if m >= 256:
+                row["value"], row["unit"] = round(alg_flops(m, n, k) / per / 1e9, 2), "GFLOP/s"
+            else:
+                row["value"], row["unit"] = round(alg_bytes(qt, m, n, k) / per / 1e9, 3), "GB/s"
+            if key in gpu_us:
+                row["gpu_us_per_call"] = round(gpu_us[key], 2)
+                row["gpu_speedup"] = round(per * 1e6 / gpu_us[key], 1)
+            rows.append(row)
+    # one decode-step layer: q, k, v, o, gate, up, down (x 28 layers)
+    layer = [(n, k, synth.make_blocks("q4_0", n, k, 6000 + i),
+              synth.make_x(1, k, 6100 + i)[0]) for i, (_, n, k) in enumerate(SWEEP_SHAPES)]
+    for flavor in flavors:
+        log(f"cpu sweep {flavor}")
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            for n, k, blocks, x in layer:
+                oracle.linear(x, blocks, (n, k), "q4_0", threads=threads, flavor=flavor)
+            reps += 1
+            if time.perf_counter() - t0 >= budget_s:
+                break
+        per = (time.perf_counter() - t0) / reps * 28
+        row = {"config": "configs[4] decode sweep (196 GEMVs)", "build": flavor, "qtype": "q4_0",
+               "us_per_call": round(per * 1e6, 1), "cores": threads,
+               "value": round(sum(alg_bytes("q4_0", 1, n, k) for _, n, k in SWEEP_SHAPES) * 28
+                              / per / 1e9, 3), "unit": "GB/s",
+               "sample": f"{reps} pass(es) over one layer's 7 GEMVs, x 28 layers"}
+        sw = result["configs"].get("sweep", {})
+        if "us_per_step" in sw:
+            row["gpu_us_per_call"] = sw["us_per_step"]
+            row["gpu_speedup"] = round(per * 1e6 / sw["us_per_step"], 1)
+        rows.append(row)
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -744,6 +865,12 @@ def main():
                     "frac": round(prefill["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                     "dtype": "fp16 MFMA, fp32 accumulate"},
     }
+    dense = bench_dense_ceiling(torch, 512, 11008, 4096, pre_steps, min(args.warmup, 5))
+    result["prefill"]["mfma_ceiling"] = {
+        "what": "dense fp16 / bf16 GEMM of the same shape through torch.matmul (hipBLASLt), "
+                "no weight decode, weights rotated like the quantized case",
+        **dense,
+        "ours_vs_fp16": round(dense["fp16"]["us_per_call"] / prefill["us_per_call"], 3)}
     pre8 = bench_int8(pkg, torch, 512, 11008, 4096, pre_steps, min(args.warmup, 5), seed=4000)
     result["prefill_int8"] = {
         "workload": "configs[4] int8 variant: X quantized to q8_0 (quantizeToQ80 rules) "
@@ -780,6 +907,17 @@ def main():
         extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
                        for kk, v in r.items()}
         extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
+    # "LLC-hot": one weight copy, resident in the 256 MB Infinity Cache after
+    # the warm-up launches; not an HBM figure
+    hot = {}
+    for name, qt, m, n, k in [("c0", "q8_0", 1, 4096, 4096), ("c1", "q4_0", 1, 18944, 3584),
+                              ("c2", "q4_1", 1, 4096, 14336), ("c3_m4", "q4_0", 4, 4096, 4096),
+                              ("c3_m16", "q4_0", 16, 4096, 4096),
+                              ("c3_m64", "q4_0", 64, 4096, 4096)]:
+        r = bench_case(pkg, torch, qt, m, n, k, args.steps, args.warmup, 100, rotate=False)
+        hot[name] = {"us_per_call": round(r["us_per_call"], 3), "gbs": round(r["gbs"], 1)}
+    extra["llc_hot"] = {"what": "single weight copy re-read every call (Infinity-Cache "
+                                "resident): LLC-hot, not HBM bandwidth", **hot}
     # raw GGUF block pointers (mlq_linear_aos, the reference's device-weight
     # meaning) at configs[1] and configs[0]
     extra["c1_aos"] = bench_aos(pkg, torch, "q4_0", 1, 18944, 3584, args.steps,
@@ -823,21 +961,10 @@ def main():
             curve[str(t)] = round(v["value"], 3)
         curve[str(threads)] = result["cpu_baseline"]["value"]
         result["cpu_baseline"]["gbs_by_threads"] = curve
-        # the same CPU path with and without the reference's AVX2 build, on
-        # the headline shape and on configs[0] (q8_0, the type with an AVX2
-        # loop), a few seconds each
-        oracle = graft.load_oracle()
-        variants = []
-        for qt, n, k, tag in (("q4_0", 18944, 3584, "configs[1]"),
-                              ("q8_0", 4096, 4096, "configs[0]")):
-            for flavor in ("scalar", "avx2"):
-                if (qt, flavor) == ("q4_0", "scalar") or not oracle.flavor_available(flavor):
-                    continue
-                v = cpu_baseline(qt, n, k, min(3.0, args.cpu_budget), flavor, threads)
-                variants.append({"config": tag, "build": flavor,
-                                 "value": round(v["value"], 3), "unit": "GB/s",
-                                 "cores": v["cores"], "sample": v["sample"]})
-        result["cpu_baseline_builds"] = variants
+        # every BASELINE workload with and without the reference's AVX2
+        # build, beside this run's GPU times
+        result["cpu_baseline_builds"] = cpu_all_configs(result, threads,
+                                                         min(1.0, args.cpu_budget))
     print(json.dumps(result), flush=True)
 
 

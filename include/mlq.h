@@ -177,8 +177,12 @@ int mlq_linear_ws(const mlq_weight* w, const float* x, float* y, int m,
  * fp32 x (src/quant.cc:505-628, src/cuda_quant.cu:78-128); this variant adds
  * the activation quantization error (at most d/2 = max|x in block| / 254
  * per element), which grows like sqrt(k) against the tolerance's k: it
- * meets the Linear's tolerance on N(0,1)-like rows from k ~ 1000 on. Needs
- * |x| < 127 * 65504 (finite block scales); any m >= 1. Workspace: device,
+ * meets the Linear's tolerance on N(0,1)-like rows from k ~ 1000 on. Range:
+ * a 32-element block of x whose largest |x| reaches 127 * 65520 gets an
+ * infinite fp16 scale and all-zero codes under quantizeToQ80's rules, and
+ * every output of that row is then NaN (inf * 0), as the product with the
+ * dequantized q8_0 block is; below that every finite x works (mlq_linear,
+ * the fp16 path, has no such limit). Any m >= 1. Workspace: device,
  * 256-byte aligned
  * (else MLQ_ERR_INVALID_ARG), at least mlq_linear_q8act_workspace(w, m)
  * bytes (not NULL). No counterpart in the reference (no int8 kernel exists

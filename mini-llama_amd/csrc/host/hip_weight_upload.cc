@@ -138,6 +138,16 @@ void uploadF32LinearWeight(HipModelWeights& storage,
 void uploadF32TensorWeight(HipModelWeights& storage, const Tensor& weight,
                            const std::string& name, int device_id) {
   if (weight.data.empty()) return;
+  // data must hold the shape's element count (the reference's message,
+  // src/cuda_weight_upload.cc:75-81, whose comparison of data.size() with
+  // size() == data.size() cannot fail; the shape product is what it names)
+  size_t expected = weight.shape.empty() ? weight.data.size() : 1;
+  for (const int d : weight.shape) expected *= (size_t)(d > 0 ? d : 0);
+  if (weight.data.size() != expected) {
+    throw std::runtime_error("HIP weight upload: tensor data size mismatch for " + name +
+                             ", expected " + std::to_string(expected) + ", got " +
+                             std::to_string(weight.data.size()));
+  }
   const size_t bytes = weight.data.size() * sizeof(float);
   HipUploadedWeight uploaded;
   uploaded.name = name;

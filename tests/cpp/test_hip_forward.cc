@@ -37,6 +37,7 @@
 #include "mini_llama/hip_quant.h"
 #include "mini_llama/hip_runtime.h"
 #include "mini_llama/hip_tensor.h"
+#include "mini_llama/hip_model_upload.h"
 #include "mini_llama/hip_weight_upload.h"
 #include "mini_llama/model_config.h"
 #include "quant_ref.h"
@@ -228,11 +229,64 @@ QuantizedTensor linearWeight(const Tensor& w, const std::string& quant) {
   return q;
 }
 
+// The reference's MiniLlamaModel weight fields (include/mini_llama/model.h:
+// 37-61), with the hip_weights member a --backend hip build adds: what
+// uploadModelWeightsToHip takes.
+struct HostLayerWeights {
+  Tensor attention_norm;
+  QuantizedTensor wq, wk, wv;
+  Tensor bq, bk, bv;
+  QuantizedTensor wo;
+  Tensor ffn_norm;
+  QuantizedTensor w_gate, w_up, w_down;
+};
+
+struct HostModel {
+  bool loaded = false;
+  Tensor token_embedding;
+  std::vector<HostLayerWeights> layers;
+  Tensor final_norm;
+  QuantizedTensor lm_head;
+  std::shared_ptr<HipModelWeights> hip_weights;
+};
+
+// The manifest model with its Linear weights quantized as asked
+// (quantizeModelToQ80 / Q40's role, src/model.cc:107-148).
+HostModel hostModel(const Model& m, const std::string& quant) {
+  HostModel h;
+  auto get = [&](const std::string& name) {
+    const auto it = m.tensors.find(name);
+    return it == m.tensors.end() ? Tensor() : it->second;
+  };
+  h.token_embedding = get("token_embedding");
+  h.final_norm = get("final_norm");
+  h.lm_head = linearWeight(get("lm_head"), quant);
+  for (int i = 0; i < m.c.n_layers; ++i) {
+    const std::string p = "layers." + std::to_string(i) + ".";
+    HostLayerWeights lw;
+    lw.attention_norm = get(p + "attention_norm");
+    lw.wq = linearWeight(get(p + "wq"), quant);
+    lw.wk = linearWeight(get(p + "wk"), quant);
+    lw.wv = linearWeight(get(p + "wv"), quant);
+    lw.bq = get(p + "bq");
+    lw.bk = get(p + "bk");
+    lw.bv = get(p + "bv");
+    lw.wo = linearWeight(get(p + "wo"), quant);
+    lw.ffn_norm = get(p + "ffn_norm");
+    lw.w_gate = linearWeight(get(p + "w_gate"), quant);
+    lw.w_up = linearWeight(get(p + "w_up"), quant);
+    lw.w_down = linearWeight(get(p + "w_down"), quant);
+    h.layers.push_back(std::move(lw));
+  }
+  h.loaded = true;
+  return h;
+}
+
 // ---- forwardToken's device branch ---------------------------------------------
 struct Engine {
-  explicit Engine(const Model& m) : model(m) {}
+  Engine(const Model& m, const HipModelWeights& uploaded) : model(m), weights(uploaded) {}
   const Model& model;
-  HipModelWeights weights;
+  const HipModelWeights& weights;
   HipKvCache cache;
   int dev = 0;
 
@@ -301,20 +355,32 @@ int main(int argc, char** argv) {
     const std::string quant = argv[3];
     std::vector<int> tokens;
     for (int i = 5; i < argc; ++i) tokens.push_back(std::atoi(argv[i]));
-    Engine eng(model);
     const ModelConfig& c = model.c;
-    // uploadModelWeightsToCuda (src/model.cc:151-199): every Linear, plus the
-    // embedding, norms and biases as plain F32 tensors
-    for (const auto& [name, t] : model.tensors) {
-      const bool is_linear = name == "lm_head" || name.find(".w") != std::string::npos;
-      if (is_linear) {
-        const QuantizedTensor q = linearWeight(t, quant);
-        uploadLinearWeight(eng.weights, q, name, 0);
-        eng.linearType = q.type;
-      } else {
-        uploadF32TensorWeight(eng.weights, t, name, 0);
-      }
+    // uploadModelWeightsToCuda's twin (src/model.cc:151-199): every Linear,
+    // plus the embedding, norms and biases as plain F32 tensors
+    HostModel host = hostModel(model, quant);
+    HostModel unloaded;
+    bool threw = false;
+    try {
+      uploadModelWeightsToHip(unloaded, 0);
+    } catch (const std::runtime_error&) {
+      threw = true;
     }
+    if (!threw || modelHasHipWeights(unloaded))
+      throw std::runtime_error("upload of an unloaded model did not throw");
+    uploadModelWeightsToHip(host, 0);
+    // 3 global weights + per layer 2 norms, 7 Linear weights and the biases
+    // the manifest holds
+    size_t expected = 3;
+    for (const HostLayerWeights& lw : host.layers)
+      expected += 9 + !lw.bq.data.empty() + !lw.bk.data.empty() + !lw.bv.data.empty();
+    if (!modelHasHipWeights(host) || modelHipUploadedWeightCount(host) != expected ||
+        modelHipMemoryBytes(host) == 0)
+      throw std::runtime_error("uploadModelWeightsToHip: " +
+                               std::to_string(modelHipUploadedWeightCount(host)) +
+                               " weights uploaded, expected " + std::to_string(expected));
+    Engine eng(model, *host.hip_weights);
+    eng.linearType = host.lm_head.type;
     eng.cache.reset(c.n_layers, c.max_seq_len, c.n_kv_heads, c.head_dim, 0);
     std::ofstream out(argv[4], std::ios::binary);
     for (size_t i = 0; i < tokens.size(); ++i) {

@@ -5,9 +5,11 @@ Everything here calls libmlq through its C ABI (ctypes); the oracle
   - dequantization: bit-exact (integer/byte work and exact d*q products);
   - Linear outputs: the stated tolerance (tests/conftest.py), plus the
     reference CUDA tests' 1e-4 absolute bound on their own inputs;
-  - full benchmark shapes: oracle on sampled output rows.
+  - full benchmark shapes: every output against the oracle.
 """
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -486,6 +488,44 @@ def test_fused_swiglu(pkg, oracle, cuda, qtype, m, ffn, k):
     assert np.all((err <= bound) | (err <= 2e-3 * np.abs(ro))), err.max()
 
 
+@pytest.mark.parametrize("m", [9, 16])
+def test_swiglu_two_tile_skinny_odd_tiles(pkg, oracle, cuda, m):
+    """The fp32-x skinny kernel with two weight tiles per workgroup (the
+    default plan for q4_0 at 9..16 rows when it saves a round of workgroups)
+    on an odd tile count (8208 rows = 513 tiles: the last workgroup holds one
+    tile) with the bias + SwiGLU epilogue: forced two-tile and one-tile plans
+    agree with each other and with the oracle."""
+    torch = _torch()
+    qtype, ffn, k = "q4_0", 4104, 256
+    _print_case(test="swiglu_t2", m=m, ffn=ffn, k=k)
+    gate = make_blocks(qtype, ffn, k, seed=ffn + 7)
+    up = make_blocks(qtype, ffn, k, seed=ffn + 8)
+    x = make_x(m, k, seed=k + 9)
+    xd = _dev(x, cuda)
+    bg = make_x(1, ffn, seed=ffn + 4)[0]
+    bu = make_x(1, ffn, seed=ffn + 5)[0]
+    tw = pkg.upload_glu(qtype, gate, up, ffn, k, device=cuda)
+    bias = torch.from_numpy(pkg.interleave_rows(bg, bu, ffn)).to(cuda)
+    outs = {}
+    try:
+        for tiles in (2, 1):
+            pkg.set_skinny_plan(tiles, 0)
+            outs[tiles] = pkg.linear(tw, xd, bias=bias, act=pkg.EPI_SWIGLU).cpu().numpy()
+    finally:
+        pkg.set_skinny_plan(0, 0)
+    default = pkg.linear(tw, xd, bias=bias, act=pkg.EPI_SWIGLU).cpu().numpy()
+    assert outs[2].shape == (m, ffn)
+    assert np.array_equal(outs[2], outs[1])
+    assert np.array_equal(default, outs[2])
+    go = oracle.linear(x, gate, (ffn, k), qtype).astype(np.float64) + bg
+    uo = oracle.linear(x, up, (ffn, k), qtype).astype(np.float64) + bu
+    ro = _silu64(go) * uo
+    atol = 1e-3 * np.linalg.norm(x, axis=1, keepdims=True) * np.sqrt(k / 4096)
+    bound = (1.1 * np.abs(uo) + np.abs(_silu64(go))) * atol + 1.1 * atol * atol
+    err = np.abs(outs[2] - ro)
+    assert np.all((err <= bound) | (err <= 2e-3 * np.abs(ro))), err.max()
+
+
 def test_gguf_upload_matches_host_repack(pkg, oracle, cuda, tmp_path):
     """Tensors uploaded straight from a mapped GGUF file (device copy +
     device repack) are the same tiled bytes as the host repack of the same
@@ -591,35 +631,39 @@ def test_validation_errors(pkg, cuda):
 
 
 # --------------------------------------------------------------------------
-# Full benchmark shapes (sampled oracle rows)
+# Full benchmark shapes: every output against the oracle
 # --------------------------------------------------------------------------
 CONFIGS = [("c0", "q8_0", 1, 4096, 4096), ("c1", "q4_0", 1, 18944, 3584),
            ("c2", "q4_1", 1, 4096, 14336), ("c3", "q4_0", 4, 4096, 4096),
            ("c3", "q4_0", 16, 4096, 4096), ("c3", "q4_0", 64, 4096, 4096),
            ("c4", "q8_0", 512, 11008, 4096),
-           # decode-sweep shapes: K = 18944 takes the GEMV refill ring,
-           # N = 37888 is the fused gate|up weight
+           # the decode sweep's seven shapes: q and o [3584, 3584],
+           # k and v [512, 3584], gate and up [18944, 3584] (= c1), down
+           # [3584, 18944] (K = 18944 takes the GEMV refill ring), and the
+           # fused gate|up weight N = 37888
+           ("q/o", "q4_0", 1, 3584, 3584), ("k/v", "q4_0", 1, 512, 3584),
            ("down", "q4_0", 1, 3584, 18944), ("gateup", "q4_0", 1, 37888, 3584)]
 
 
 @pytest.mark.parametrize("cfg,qtype,m,n,k", CONFIGS)
 def test_config_shapes(pkg, oracle, cuda, cfg, qtype, m, n, k):
+    """Every output of each BASELINE workload through the benchmarked entry
+    point (mlq_linear_epi with the per-device workspace: the fp16 copy and
+    the prefill GEMM for c4, the skinny GEMM for M = 16 / 64, the GEMV
+    below), compared with the reference CPU Linear (the oracle, all output
+    rows and columns, the reference thread partition), as the reference's
+    CUDA tests compare every element (tests/test_cuda.cc:679-743)."""
     _print_case(test="config", cfg=cfg, qtype=qtype, m=m, n=n, k=k)
     blocks = make_blocks(qtype, n, k, seed=1000 + n)
     x = make_x(m, k, seed=2000 + m)
     tw = pkg.upload(qtype, blocks, n, k, device=cuda)
-    y = pkg.linear(tw, _dev(x, cuda)).cpu().numpy()
+    y = pkg.linear(tw, _dev(x if m > 1 else x[0], cuda)).cpu().numpy().reshape(m, n)
     assert np.isfinite(y).all()
-    rng = np.random.default_rng(m + n)
-    rows = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, 64)]))
-    nb = (k + 31) // 32
-    ms = np.arange(m) if m <= 8 else np.unique(
-        np.concatenate([[0, m - 1], rng.integers(0, m, 6)]))
-    xs = x[ms]
-    for r in rows:
-        ref = oracle.linear(xs, blocks[r * nb:(r + 1) * nb], (1, k), qtype)
-        got = y[ms][:, [r]]
-        assert tolerance_ok(got, ref, xs, k).all(), (r, error_report(got, ref, xs, k))
+    threads = max(1, min(16, os.cpu_count() or 1))
+    ref = oracle.linear(x, blocks, (n, k), qtype, threads=threads)
+    ok = tolerance_ok(y, ref, x, k)
+    bad = np.argwhere(~ok)
+    assert ok.all(), (len(bad), bad[:8].tolist(), error_report(y, ref, x, k))
 
 
 def test_linearity_full_c1(pkg, cuda):

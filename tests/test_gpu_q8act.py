@@ -109,6 +109,32 @@ def test_q8act_special_rows_and_codes(pkg, oracle, cuda):
     _check_all(pkg, oracle, cuda, x, blocks, n, k, fp32_check=False)
 
 
+def test_q8act_block_scale_overflow(pkg, oracle, cuda):
+    """The range edge of the q8_0 activation scale d = fp16(max|x| / 127):
+    a block whose largest |x| is 8.3e6 keeps a finite scale (65344) and the
+    row meets every check; a block at 1e7 overflows d to inf, its codes are
+    all zero (x * (1 / inf)), and the whole output row is NaN (inf * 0), as
+    the product with the dequantized block is. Other rows are unaffected."""
+    m, n, k = 8, 64, 1000
+    _case(test="q8act_overflow", m=m, n=n, k=k)
+    x = make_x(m, k, seed=31)
+    x[3, 37] = 8.3e6
+    x[5, 200] = -1.0e7
+    blocks = make_blocks("q8_0", n, k, seed=32)
+    # the quantizer's side of the edge, on the CPU
+    xq = oracle.quantize(x, "q8_0").reshape(m, -1)
+    d = oracle.fp16_to_f32(xq["d"])
+    assert np.isfinite(d[3]).all() and d[3, 37 // 32] == np.float32(65344.0)
+    assert np.isinf(d[5, 200 // 32]) and (xq["qs"][5, 200 // 32] == 0).all()
+    tw = pkg.upload("q8_0", blocks, n, k, device=cuda)
+    got = _run(pkg, cuda, tw, x).reshape(m, n)
+    assert np.isnan(got[5]).all()
+    keep = [r for r in range(m) if r != 5]
+    _check_all(pkg, oracle, cuda, x[keep], blocks, n, k)
+    ref_rows = _run(pkg, cuda, tw, np.ascontiguousarray(x[keep])).reshape(len(keep), n)
+    assert np.array_equal(got[keep], ref_rows)
+
+
 def test_q8act_workspace_contract(pkg, cuda):
     import torch
     m, n, k = 5, 32, 64
