@@ -118,6 +118,13 @@ __device__ __forceinline__ uint32_t buf_load4(rsrc_t r, uint32_t voff,
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
 }
 
+// 32-bit store through a buffer resource: offsets past the range are
+// dropped (no write, no fault).
+__device__ __forceinline__ void buf_store4(float v, rsrc_t r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)voff, (int)soff,
+                                        0);
+}
+
 // Two fp32 -> packed fp16 pair (round to nearest even).
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   h2_t h;
