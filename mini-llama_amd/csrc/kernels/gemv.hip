@@ -15,17 +15,26 @@
 //    offset per group, and anything past the wave's range (ragged K tails,
 //    the groups of a shorter last slice) reads as zero with no branches.
 //  - Order of issue: the wave's activation slice first, then the weight
-//    lines of its first groups (GW = groups per wave, a compile-time
+//    lines of its first two groups (GW = groups per wave, a compile-time
 //    1..10), then the fp32 -> fp16 hi/lo conversion of the activations into
 //    the wave's private LDS slice, then the remaining weight lines. All
 //    waves start within ~0.5 us and the activation lines miss L2: issued
 //    behind every weight line of the slice they queue behind tens of MB of
 //    weight requests (measured: half the waves of the 4096 x 14336 q4_1
-//    GEMV staged x only after 5 us). Slices of 6+ groups and ring slices
-//    therefore stage x before any weight load (that shape 12.4 -> 10.2 us,
-//    3584 x 18944 q4_0 19.4 -> 15.7 us); shorter slices issue two groups
-//    first, which keeps HBM busy during the activation fetch (1-3 % faster
-//    than all groups first at 4 groups per wave, 3-8 % faster than x-first).
+//    GEMV staged x only after 5 us with all groups first). Two groups ahead
+//    keep HBM busy during the activation fetch without that queueing: 1-3 %
+//    faster than all groups first at 4 groups per wave, and faster than no
+//    group ahead at every depth (4096 x 14336 q4_1 10.03 -> 9.85 us,
+//    3584 x 18944 q4_0 10.75 -> 10.35, the decode step 1459 -> 1415 us).
+//    Ring slices stage x before any weight load.
+//  - Grids of about one workgroup per CU also hold every weight load until
+//    all waves of the workgroup have issued their activation loads (one
+//    s_barrier, no wait): the later waves' activation lines then no longer
+//    queue behind the earlier waves' first groups (4096 x 4096 q4_0 at
+//    M = 4 5.16 -> 4.82 us, the 7B q|k|v 5.03 -> 4.87). Grids of several
+//    rounds (the 1184-tile 18944 x 3584 GEMV 8.80 -> 8.92 us) and q8_0 at
+//    one row, whose activations are a small part of a wave's reads
+//    (4096 x 4096 4.93 -> 4.99), run without it.
 //    The group loop has no data-dependent branch: a shorter last slice
 //    processes zero groups (zero scales, zero activations). Slices longer
 //    than the register budget run a ring of GW slots instead (GW chosen to
@@ -102,6 +111,7 @@ struct GemvArgs {
   int wave_lds;  // bytes of LDS per wave (activation slice + block sums)
   Epilogue epi;
   int ny;        // output columns: n, or n/2 under kEpiSwiGLU
+  int xbar;      // 1: weight loads wait until every wave issued its activation loads
 };
 
 template <int QT>
@@ -329,8 +339,13 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // Issued group by group (not clustered by kind), so group 0 can start as
   // soon as its own line and scales land. The other groups of the first GW
   // follow the activation staging (see the order of issue above).
+  if (a.xbar) {  // workgroup-uniform
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
   Slot<QT> ring[GW];
-  constexpr int kPre = (RING || GW >= 6) ? 0 : (GW < 2 ? GW : 2);
+  constexpr int kPre = RING ? 0 : (GW < 2 ? GW : 2);
 #pragma unroll
   for (int s = 0; s < kPre; ++s) {
     load_group<QT>(rs, ring[s], s, qoff, soff);
@@ -968,6 +983,13 @@ hipError_t launch_gemv(const mlq_weight& w, const float* x, float* y, int m,
   a.wave_lds = (int)p.wave_lds;
   a.epi = epi;
   a.ny = epi.act == kEpiSwiGLU ? w.n / 2 : w.n;
+  // Activation loads ahead of every weight load of the workgroup: for grids
+  // of at most ~1.25 workgroups per CU whose waves read at least a third as
+  // many activation bytes as weight bytes (all but q8_0 at one row).
+  const int unit_bytes = (w.type == MLQ_Q8_0 ? 2048 : 1024) + kUnitScaleBytes +
+                         (w.type == MLQ_Q4_1 ? kUnitScaleBytes : 0);
+  a.xbar = p.split > 1 && 4 * (long)geo.nt <= 5 * (long)device_cus() &&
+           3 * m * kGroupK * 4 >= unit_bytes;
   switch (w.type) {
     case MLQ_Q8_0: return launch_rows<MLQ_Q8_0>(a, p, stream);
     case MLQ_Q4_0: return launch_rows<MLQ_Q4_0>(a, p, stream);
