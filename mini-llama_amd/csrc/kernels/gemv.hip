@@ -284,10 +284,15 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   const int c4 = npad * (kGroupK / 4);
   const uint32_t xbytes = (uint32_t)min(ng * kGroupK, a.k - kbase) * 4u;
   constexpr bool vec = VEC;
-  // Register-held part: MR == 1 covers 4 float4 per lane (8 groups); MR > 1
-  // covers one float4 per lane of every row (2 groups). The rest, if any,
-  // is loaded and staged in a second pass.
-  constexpr int XR = MR == 1 ? kXRegs : kGemvMaxRows;
+  // Register-held part: MR == 1 covers the whole slice of a non-ring wave
+  // (one float4 per lane per two groups, at least 4), 8 groups for ring
+  // slices; MR > 1 covers one float4 per lane of every row (2 groups). The
+  // rest, if any, is read twice more (its maximum, then the staging): each
+  // a round trip that every weight load after the staging waits for (the
+  // 3584 x 18944 down projection at 10 groups per wave staged at 4.4 us
+  // median with 8 groups held, against ~1.3 us for 4-group slices).
+  constexpr int XR = MR == 1 ? (!RING && GW > 2 * kXRegs ? (GW + 1) / 2 : kXRegs)
+                             : kGemvMaxRows;
   // Input RMSNorm (one row): the norm weight is loaded beside x, the staged
   // values are x * weight and the lanes keep sum(x^2) of their elements.
   // (its register-held part is loaded with x: reading it at staging time
