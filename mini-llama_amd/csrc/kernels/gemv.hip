@@ -31,7 +31,10 @@
 //    all waves of the workgroup have issued their activation loads (one
 //    s_barrier, no wait): the later waves' activation lines then no longer
 //    queue behind the earlier waves' first groups (4096 x 4096 q4_0 at
-//    M = 4 5.16 -> 4.82 us, the 7B q|k|v 5.03 -> 4.87). Grids of several
+//    M = 4 5.16 -> 4.82 us, the 7B q|k|v 5.03 -> 4.87). With one
+//    activation row these grids then issue one group ahead instead of two
+//    (q|k|v 4.96 -> 4.72 us, 4096 x 14336 q4_1 9.77 -> 9.44, the down
+//    projection 9.54 -> 9.31; M = 4 keeps two: 4.74 vs 4.96). Grids of several
 //    rounds (the 1184-tile 18944 x 3584 GEMV 8.80 -> 8.92 us) and q8_0 at
 //    one row, whose activations are a small part of a wave's reads
 //    (4096 x 4096 4.93 -> 4.99), run without it.
@@ -340,23 +343,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     return float4{v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w};
   };
 
-  // ---- weight loads: the slice's first kPre groups ------------------------
-  // Issued group by group (not clustered by kind), so group 0 can start as
-  // soon as its own line and scales land. The other groups of the first GW
-  // follow the activation staging (see the order of issue above).
-  if (a.xbar) {  // workgroup-uniform
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  Slot<QT> ring[GW];
-  constexpr int kPre = RING ? 0 : (GW < 2 ? GW : 2);
-#pragma unroll
-  for (int s = 0; s < kPre; ++s) {
-    load_group<QT>(rs, ring[s], s, qoff, soff);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
   // ---- per-row scale of the slice ------------------------------------------
   // Every activation row of the slice is staged as x * 2^e, so any finite
   // fp32 row fits the fp16 hi/lo pair: e = 0 while the row's largest |x| in
@@ -368,11 +354,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // Slices longer than the register-held part (MR == 1: > 8 groups; MR > 1:
   // > 2 groups) read the rest once for the maximum and once to stage it.
   const int c_done = MR == 1 ? 64 * XR : 64;
-  if constexpr (norm) {
-#pragma unroll
-    for (int i = 0; i < XR; ++i)
-      if (64 * i < c4) xr[i] = normed(xr[i], gr[i]);  // wave-uniform
-  }
   // this lane's largest |x| of row r in the register-held part
   auto reg_max = [&](int r) __attribute__((always_inline)) {
     float mx = 0.0f;
@@ -470,37 +451,78 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // tolerance. The slice is staged with scale 1 right away while a
   // wave-wide vote checks the window; only when a row falls outside it do
   // the rows pay for their exact maxima (a cross-lane reduction) and a
-  // second, scaled staging pass.
-  stage(std::false_type{});
-  // Per lane: bit r = row r has a value >= 2^-10 here, bit 31 = some row
-  // has a value >= 2^15 here; one OR across the wave (VALU and a few scalar
-  // instructions: the scalar unit is shared by the CU's waves).
-  uint32_t flags = 0;
+  // second, scaled staging pass. Returns whether every row kept scale 1.
+  auto stage_slice = [&]() __attribute__((always_inline)) {
+    if constexpr (norm) {
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    if (r >= M) break;  // wave-uniform
-    const float mx = reg_max(r);
-    flags |= (mx >= 0x1p-10f ? 1u << r : 0u) | (mx >= 0x1p15f ? 1u << 31 : 0u);
-  }
-  if (c4 > c_done) {
+      for (int i = 0; i < XR; ++i)
+        if (64 * i < c4) xr[i] = normed(xr[i], gr[i]);  // wave-uniform
+    }
+    stage(std::false_type{});
+    // Per lane: bit r = row r has a value >= 2^-10 here, bit 31 = some row
+    // has a value >= 2^15 here; one OR across the wave (VALU and a few scalar
+    // instructions: the scalar unit is shared by the CU's waves).
+    uint32_t flags = 0;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       if (r >= M) break;  // wave-uniform
-      const float mx = rest_max(r);
+      const float mx = reg_max(r);
       flags |= (mx >= 0x1p-10f ? 1u << r : 0u) | (mx >= 0x1p15f ? 1u << 31 : 0u);
     }
-  }
-  const uint32_t all = wave_or(flags);
-  const bool unit = all == ((1u << M) - 1u);
-  if (!unit) {
+    if (c4 > c_done) {
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      if (r >= M) break;  // wave-uniform
-      float mx = reg_max(r);
-      if (c4 > c_done) mx = fmaxf(mx, rest_max(r));
-      ex[r] = __builtin_amdgcn_readfirstlane(pow2_scale_exp(wave_max_nonneg(mx)));
+      for (int r = 0; r < NR; ++r) {
+        if (r >= M) break;  // wave-uniform
+        const float mx = rest_max(r);
+        flags |= (mx >= 0x1p-10f ? 1u << r : 0u) | (mx >= 0x1p15f ? 1u << 31 : 0u);
+      }
     }
-    stage(std::true_type{});
+    const uint32_t all = wave_or(flags);
+    const bool unit = all == ((1u << M) - 1u);
+    if (!unit) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        if (r >= M) break;  // wave-uniform
+        float mx = reg_max(r);
+        if (c4 > c_done) mx = fmaxf(mx, rest_max(r));
+        ex[r] = __builtin_amdgcn_readfirstlane(pow2_scale_exp(wave_max_nonneg(mx)));
+      }
+      stage(std::true_type{});
+    }
+    return unit;
+  };
+
+  // ---- weight loads around the staging --------------------------------------
+  // Issued group by group (not clustered by kind), so group 0 can start as
+  // soon as its own line and scales land. Non-ring slices issue two groups
+  // ahead of the staging, or, in grids of one round (xbar), hold every
+  // weight load until all waves of the workgroup issued their activation
+  // loads and then issue one (one activation row) or two (see the order of
+  // issue above). Both orders are written out so that each path's wait
+  // counts stay exact.
+  Slot<QT> ring[GW];
+  constexpr int kPre = RING ? 0 : (GW < 2 ? GW : 2);
+  constexpr int kPreX = MR == 1 ? (kPre < 1 ? kPre : 1) : kPre;  // xbar path
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    load_group<QT>(rs, ring[s], s, qoff, soff);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if (a.xbar) {  // workgroup-uniform
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  bool unit;
+  if (kPreX < kPre && a.xbar) {
+#pragma unroll
+    for (int s = 0; s < kPreX; ++s) issue(s);
+    unit = stage_slice();
+#pragma unroll
+    for (int s = kPreX; s < kPre; ++s) issue(s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kPre; ++s) issue(s);
+    unit = stage_slice();
   }
   // ---- weight loads: the rest of the first GW groups ------------------------
   __builtin_amdgcn_sched_barrier(0);
