@@ -612,6 +612,27 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     }
   }
 
+  // The bias (or residual) entries of the rows this thread writes, requested
+  // before the slices combine: loaded after the final barrier they added a
+  // memory round trip to the tail of every workgroup, and requested with
+  // the activations they held registers through the group loop. Row
+  // tile*16 + (tid & 15); under SwiGLU with several slices the thread
+  // writes gate row (tid & 7) and up row (tid & 7) + 8. Only waves 0 and 1
+  // write outputs (the other waves' loads move no data); rows past n read
+  // zero, as does everything without a bias (an empty range: no branch).
+  __builtin_amdgcn_sched_barrier(0);
+  const bool has_bias = a.epi.bias != nullptr;
+  const rsrc_t rb = make_rsrc(has_bias ? a.epi.bias + (size_t)tile * kTileRows : a.y,
+                              has_bias && wave < 2
+                                  ? (uint32_t)min(kTileRows, a.n - tile * kTileRows) * 4u
+                                  : 0u);
+  const bool pairs = a.epi.act == kEpiSwiGLU && a.split > 1;
+  const uint32_t bc = pairs ? (uint32_t)(tid & 7) : (uint32_t)(tid & 15);
+  const float bias0 = __builtin_bit_cast(float, buf_load4(rb, bc * 4u, 0));
+  const float bias8 = __builtin_bit_cast(float, buf_load4(rb, (bc + 8u) * 4u, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  auto biased = [&](float v, float b) { return a.epi.bias != nullptr ? v + b : v; };
+
   // ---- output ------------------------------------------------------------
   // undo the slice's power-of-two scale of activation rows r0 and r1
   if (!unit) {
@@ -644,8 +665,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       acc0 = acc0 / nscale;
       acc1 = acc1 / nscale;
     }
-    const float v0 = add_bias(a.epi, acc0, min(row, a.n - 1));
-    const float v1 = add_bias(a.epi, acc1, min(row, a.n - 1));
+    const float v0 = biased(acc0, bias0);
+    const float v1 = biased(acc1, bias0);
     if (can_produce && a.epi.next_x != nullptr) {  // one row, no activation
       produce_norm_input(a, tile, lane, kq == 0 && row < a.n ? v0 : 0.0f, gnext);
       if (kq == 0 && row < a.n) a.y[row] = v0;
@@ -690,7 +711,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     if (wave == 0) {
       const int row = tile * kTileRows + (lane & 15);
       const bool live = lane < kTileRows && row < a.n;
-      const float v = live ? add_bias(a.epi, slice_sum(0, lane & 15), row) : 0.0f;
+      const float v = live ? biased(slice_sum(0, lane & 15), bias0) : 0.0f;
       produce_norm_input(a, tile, lane, v, gnext);
       if (live) a.y[row] = v;
     }
@@ -701,8 +722,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       const int r = o / 8, c = o % 8;
       const int row = tile * kTileRows + c;
       if (row >= a.n) continue;
-      const float g = add_bias(a.epi, slice_sum(r, c), row);
-      const float u = add_bias(a.epi, slice_sum(r, c + 8), row + 8);
+      const float g = biased(slice_sum(r, c), bias0);
+      const float u = biased(slice_sum(r, c + 8), bias8);
       a.y[(size_t)r * a.ny + glu_col(row)] = silu_f(g) * u;
     }
     return;
@@ -710,7 +731,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   for (int o = tid; o < M * kTileRows; o += blockDim.x) {
     const int r = o / kTileRows, nn = o % kTileRows;
     const int row = tile * kTileRows + nn;
-    if (row < a.n) a.y[(size_t)r * a.n + row] = add_bias(a.epi, slice_sum(r, nn), row);
+    if (row < a.n) a.y[(size_t)r * a.n + row] = biased(slice_sum(r, nn), bias0);
   }
 }
 
