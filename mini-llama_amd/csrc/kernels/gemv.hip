@@ -245,7 +245,10 @@ __device__ __forceinline__ void produce_norm_input(const GemvArgs& a, int tile, 
 // NM: input RMSNorm mode (one activation row): 0 none, 1 folded (the norm
 // weight is loaded beside x and sum(x^2) taken from the staged values), 2
 // pre-scaled (x holds x * norm, sum(x^2) comes from the producer's parts).
-template <int QT, int MR, int GW, bool RING, int NM, bool VEC>
+// PB: a bias (or residual) is given and requested before the slices
+// combine (one activation row, NM 0 or 2: the decode step's projections);
+// otherwise any bias is read at the end.
+template <int QT, int MR, int GW, bool RING, int NM, bool VEC, bool PB>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int M = a.m;
@@ -612,26 +615,33 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  // The bias (or residual) entries of the rows this thread writes, requested
-  // before the slices combine: loaded after the final barrier they added a
-  // memory round trip to the tail of every workgroup, and requested with
-  // the activations they held registers through the group loop. Row
-  // tile*16 + (tid & 15); under SwiGLU with several slices the thread
-  // writes gate row (tid & 7) and up row (tid & 7) + 8. Only waves 0 and 1
-  // write outputs (the other waves' loads move no data); rows past n read
-  // zero, as does everything without a bias (an empty range: no branch).
-  __builtin_amdgcn_sched_barrier(0);
-  const bool has_bias = a.epi.bias != nullptr;
-  const rsrc_t rb = make_rsrc(has_bias ? a.epi.bias + (size_t)tile * kTileRows : a.y,
-                              has_bias && wave < 2
-                                  ? (uint32_t)min(kTileRows, a.n - tile * kTileRows) * 4u
-                                  : 0u);
-  const bool pairs = a.epi.act == kEpiSwiGLU && a.split > 1;
-  const uint32_t bc = pairs ? (uint32_t)(tid & 7) : (uint32_t)(tid & 15);
-  const float bias0 = __builtin_bit_cast(float, buf_load4(rb, bc * 4u, 0));
-  const float bias8 = __builtin_bit_cast(float, buf_load4(rb, (bc + 8u) * 4u, 0));
-  __builtin_amdgcn_sched_barrier(0);
-  auto biased = [&](float v, float b) { return a.epi.bias != nullptr ? v + b : v; };
+  // PB: the bias (or residual) entries of the rows this thread writes,
+  // requested before the slices combine: loaded after the final barrier
+  // they added a memory round trip to the tail of every workgroup, and
+  // requested with the activations they held registers through the group
+  // loop. Row tile*16 + (tid & 15); under SwiGLU with several slices the
+  // thread writes gate row (tid & 7) and up row (tid & 7) + 8. Only waves 0
+  // and 1 write outputs (the other waves' loads move no data); rows past n
+  // read zero. (A compile-time choice: a runtime branch around these loads
+  // cost the group loop registers, and empty loads without a bias cost the
+  // short GEMVs 1-3 %.)
+  float bias0 = 0.0f, bias8 = 0.0f;
+  if constexpr (PB) {
+    __builtin_amdgcn_sched_barrier(0);
+    const rsrc_t rb = make_rsrc(a.epi.bias + (size_t)tile * kTileRows,
+                                wave < 2 ? (uint32_t)min(kTileRows, a.n - tile * kTileRows) * 4u
+                                         : 0u);
+    const bool pairs = a.epi.act == kEpiSwiGLU && a.split > 1;
+    const uint32_t bc = pairs ? (uint32_t)(tid & 7) : (uint32_t)(tid & 15);
+    bias0 = __builtin_bit_cast(float, buf_load4(rb, bc * 4u, 0));
+    bias8 = __builtin_bit_cast(float, buf_load4(rb, (bc + 8u) * 4u, 0));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // output v of row `row`; b: its prefetched entry
+  auto biased = [&](float v, float b, int row) {
+    if constexpr (PB) return v + b;
+    return add_bias(a.epi, v, row);
+  };
 
   // ---- output ------------------------------------------------------------
   // undo the slice's power-of-two scale of activation rows r0 and r1
@@ -665,8 +675,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       acc0 = acc0 / nscale;
       acc1 = acc1 / nscale;
     }
-    const float v0 = biased(acc0, bias0);
-    const float v1 = biased(acc1, bias0);
+    const float v0 = biased(acc0, bias0, min(row, a.n - 1));
+    const float v1 = biased(acc1, bias0, min(row, a.n - 1));
     if (can_produce && a.epi.next_x != nullptr) {  // one row, no activation
       produce_norm_input(a, tile, lane, kq == 0 && row < a.n ? v0 : 0.0f, gnext);
       if (kq == 0 && row < a.n) a.y[row] = v0;
@@ -711,7 +721,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
     if (wave == 0) {
       const int row = tile * kTileRows + (lane & 15);
       const bool live = lane < kTileRows && row < a.n;
-      const float v = live ? biased(slice_sum(0, lane & 15), bias0) : 0.0f;
+      const float v = live ? biased(slice_sum(0, lane & 15), bias0, row) : 0.0f;
       produce_norm_input(a, tile, lane, v, gnext);
       if (live) a.y[row] = v;
     }
@@ -722,8 +732,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       const int r = o / 8, c = o % 8;
       const int row = tile * kTileRows + c;
       if (row >= a.n) continue;
-      const float g = biased(slice_sum(r, c), bias0);
-      const float u = biased(slice_sum(r, c + 8), bias8);
+      const float g = biased(slice_sum(r, c), bias0, row);
+      const float u = biased(slice_sum(r, c + 8), bias8, row + 8);
       a.y[(size_t)r * a.ny + glu_col(row)] = silu_f(g) * u;
     }
     return;
@@ -731,7 +741,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   for (int o = tid; o < M * kTileRows; o += blockDim.x) {
     const int r = o / kTileRows, nn = o % kTileRows;
     const int row = tile * kTileRows + nn;
-    if (row < a.n) a.y[(size_t)r * a.n + row] = biased(slice_sum(r, nn), bias0);
+    if (row < a.n) a.y[(size_t)r * a.n + row] = biased(slice_sum(r, nn), bias0, row);
   }
 }
 
@@ -852,20 +862,24 @@ Plan make_plan(int type, int m, const Geometry& geo) {
   return p;
 }
 
-template <int QT, int MR, int GW, bool RING, int NM, bool VEC>
+template <int QT, int MR, int GW, bool RING, int NM, bool VEC, bool PB>
 hipError_t launch_vec(const GemvArgs& a, size_t lds, hipStream_t stream) {
   // Opt in to more than the default 64 KiB of dynamic LDS when needed.
   const hipError_t e =
-      allow_dynamic_lds((const void*)gemv_kernel<QT, MR, GW, RING, NM, VEC>, lds);
+      allow_dynamic_lds((const void*)gemv_kernel<QT, MR, GW, RING, NM, VEC, PB>, lds);
   if (e != hipSuccess) return e;
-  gemv_kernel<QT, MR, GW, RING, NM, VEC><<<a.nt, 64 * a.split, lds, stream>>>(a);
+  gemv_kernel<QT, MR, GW, RING, NM, VEC, PB><<<a.nt, 64 * a.split, lds, stream>>>(a);
   return hipGetLastError();
 }
 
 template <int QT, int MR, int GW, bool RING, int NM>
 hipError_t launch_kernel(const GemvArgs& a, size_t lds, hipStream_t stream) {
-  if ((a.k & 3) == 0) return launch_vec<QT, MR, GW, RING, NM, true>(a, lds, stream);
-  return launch_vec<QT, MR, GW, RING, NM, false>(a, lds, stream);
+  if ((a.k & 3) == 0) {
+    if constexpr (MR == 1 && NM != 1)
+      if (a.epi.bias != nullptr) return launch_vec<QT, MR, GW, RING, NM, true, true>(a, lds, stream);
+    return launch_vec<QT, MR, GW, RING, NM, true, false>(a, lds, stream);
+  }
+  return launch_vec<QT, MR, GW, RING, NM, false, false>(a, lds, stream);
 }
 
 // The input-RMSNorm variant exists for one activation row, and not for the
