@@ -639,8 +639,8 @@ CONFIGS = [("c0", "q8_0", 1, 4096, 4096), ("c1", "q4_0", 1, 18944, 3584),
            ("c4", "q8_0", 512, 11008, 4096),
            # the decode sweep's seven shapes: q and o [3584, 3584],
            # k and v [512, 3584], gate and up [18944, 3584] (= c1), down
-           # [3584, 18944] (K = 18944 takes the GEMV refill ring), and the
-           # fused gate|up weight N = 37888
+           # [3584, 18944] (ten groups per wave, the deepest slice held
+           # whole in registers), and the fused gate|up weight N = 37888
            ("q/o", "q4_0", 1, 3584, 3584), ("k/v", "q4_0", 1, 512, 3584),
            ("down", "q4_0", 1, 3584, 18944), ("gateup", "q4_0", 1, 37888, 3584)]
 
