@@ -31,14 +31,14 @@
 //    all waves of the workgroup have issued their activation loads (one
 //    s_barrier, no wait): the later waves' activation lines then no longer
 //    queue behind the earlier waves' first groups (4096 x 4096 q4_0 at
-//    M = 4 5.16 -> 4.82 us, the 7B q|k|v 5.03 -> 4.87). With one
-//    activation row these grids then issue one group ahead instead of two
-//    (q|k|v 4.96 -> 4.72 us, 4096 x 14336 q4_1 9.77 -> 9.44, the down
-//    projection 9.54 -> 9.31; M = 4 keeps two: 4.74 vs 4.96). Grids of several
-//    rounds (the 1184-tile 18944 x 3584 GEMV 8.80 -> 8.92 us) and q8_0 at
-//    one row, whose activations are a small part of a wave's reads
-//    (4096 x 4096 4.93 -> 4.99), run without it.
-//    The group loop has no data-dependent branch: a shorter last slice
+//    M = 4 5.16 -> 4.82 us, the 7B q|k|v 5.03 -> 4.87). Grids of several
+//    rounds (the 1184-tile 18944 x 3584 GEMV 8.80 -> 8.92 us with it) and
+//    q8_0 at one row, whose activations are a small part of a wave's reads
+//    (4096 x 4096 4.93 -> 4.99), run without this barrier. With one
+//    activation row the one-round grids then issue one group ahead instead
+//    of two (q|k|v 4.96 -> 4.72 us, 4096 x 14336 q4_1 9.77 -> 9.44, the
+//    down projection 9.54 -> 9.31; M = 4 keeps two: 4.74 vs 4.96).
+//  - The group loop has no data-dependent branch: a shorter last slice
 //    processes zero groups (zero scales, zero activations). Slices longer
 //    than the register budget run a ring of GW slots instead (GW chosen to
 //    pad the slice least), each refilled GW groups ahead as soon as its
