@@ -430,13 +430,14 @@ def _silu64(g):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("m,n,k", [(1, 48, 128), (1, 300, 1001), (4, 64, 512),
-                                   (16, 8200, 256), (40, 100, 300), (130, 70, 300),
-                                   (300, 272, 640), (512, 2048, 256)])
+@pytest.mark.parametrize("m,n,k", [(1, 48, 128), (1, 300, 1001), (1, 48, 9000),
+                                   (4, 64, 512), (16, 8200, 256), (40, 100, 300),
+                                   (130, 70, 300), (300, 272, 640), (512, 2048, 256)])
 def test_fused_bias_matches_separate_add(pkg, cuda, qtype, m, n, k):
     """The bias added in every kernel's epilogue (GEMV with one and several
-    K slices, skinny, split-K reduce, prefill GEMM) equals the kernel output
-    plus the bias, bit for bit: the same single fp32 addition."""
+    K slices, with the refill ring (q4_1 at K = 9000), skinny, split-K
+    reduce, prefill GEMM) equals the kernel output plus the bias, bit for
+    bit: the same single fp32 addition."""
     torch = _torch()
     _print_case(test="bias", qtype=qtype, m=m, n=n, k=k)
     blocks = make_blocks(qtype, n, k, seed=m + n + 2 * k)
@@ -450,7 +451,7 @@ def test_fused_bias_matches_separate_add(pkg, cuda, qtype, m, n, k):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("m,ffn,k", [(1, 48, 128), (1, 520, 1001), (4, 64, 512),
+@pytest.mark.parametrize("m,ffn,k", [(1, 48, 128), (1, 520, 1001), (1, 40, 9000), (4, 64, 512),
                                      (16, 4104, 256), (40, 56, 300), (130, 40, 300),
                                      (300, 136, 640), (512, 1024, 256)])
 def test_fused_swiglu(pkg, oracle, cuda, qtype, m, ffn, k):
