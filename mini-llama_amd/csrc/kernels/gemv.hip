@@ -354,8 +354,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // slices combine. Values beyond the register-held part are read once more
   // for this maximum.
   constexpr int NR = MR == 1 ? 1 : kGemvMaxRows;
-  // Slices longer than the register-held part (MR == 1: > 8 groups; MR > 1:
-  // > 2 groups) read the rest once for the maximum and once to stage it.
+  // Slices longer than the register-held part (MR == 1: ring slices past 8
+  // groups; MR > 1: > 2 groups) read the rest once for the maximum and once
+  // to stage it.
   const int c_done = MR == 1 ? 64 * XR : 64;
   // this lane's largest |x| of row r in the register-held part
   auto reg_max = [&](int r) __attribute__((always_inline)) {
