@@ -606,6 +606,24 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
                       (size_t)kvh * HD;
   const int last = max(nt - 1, 0);
 
+  // (fused) the RoPE inputs of this thread's first q element, requested
+  // ahead of the K / V rows so that q is rotated while they are in flight
+  float qx0 = 0.0f, qx1 = 0.0f, qc = 0.0f, qsn = 0.0f;
+  bool qfirst = true;
+  const bool qlive = FUSED && (int)threadIdx.x < GMAX * HD && (int)threadIdx.x / HD < G;
+  if constexpr (FUSED) {
+    if (qlive) {
+      constexpr int H = HD / 2;
+      const int g = threadIdx.x / HD, d = threadIdx.x - g * HD;
+      const float* x = a.q + (size_t)qrow * a.q_stride + (size_t)(h0 + g) * HD;
+      const int ii = a.neox ? (d < H ? d : d - H) : (d >> 1);
+      qfirst = a.neox ? d < H : (d & 1) == 0;
+      qc = a.rope_cs[ii];
+      qsn = a.rope_cs[H + ii];
+      qx0 = qfirst ? x[d] : x[a.neox ? d - H : d - 1];
+      qx1 = qfirst ? x[a.neox ? d + H : d + 1] : x[d];
+    }
+  }
   // every load of the chunk first: K piece, V columns, the group's q
   const f4_t* kr = (const f4_t*)(a.keys + base + (size_t)min(tp, last) * row_stride + part * KD);
   f4_t kreg[KF];
@@ -628,7 +646,9 @@ __global__ __launch_bounds__(kAttnRegWaves * 64) void attn_reg_kernel(AttnArgs a
   if constexpr (FUSED) {
     const float* qraw = a.q + (size_t)qrow * a.q_stride + (size_t)h0 * HD;
     float* qf = (float*)qs;
-    for (int i = threadIdx.x; i < GMAX * HD; i += W * 64) {
+    if ((int)threadIdx.x < GMAX * HD)
+      qf[threadIdx.x] = qlive ? (qfirst ? qx0 * qc - qx1 * qsn : qx0 * qsn + qx1 * qc) : 0.0f;
+    for (int i = threadIdx.x + W * 64; i < GMAX * HD; i += W * 64) {
       const int g = i / HD;
       qf[i] = g < G ? rope_elem<HD>(qraw + (size_t)g * HD, i - g * HD, a.neox, a.rope_cs) : 0.0f;
     }
