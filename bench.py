@@ -847,7 +847,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights x fp32 activations (fp16 hi/lo MFMA, fp32 accumulate)",
+        "dtype": "q4_0 weights x fp32 activations (23-bit integer activations as fp16 digits, exact MFMA sums, fp32 accumulate)",
         "data": "synthetic (seeded; BASELINE.json distributions)",
         "config": {"workload": "configs[1]: q4_0 GEMV W[18944,3584] M=1 "
                                "(Qwen2-7B FFN-up), weights rotated over "

@@ -1,8 +1,9 @@
 """GPU: the quantized Linear accepts any finite fp32 activation, as the
 reference's fp32 CPU loop does (src/quant.cc:459-469): every kernel path
-carries a row's activations in fp16 (hi/lo pairs in the GEMV, one rounding
-in the skinny and prefill GEMMs) scaled by a power of two chosen from the
-row's largest magnitude, and scales the fp32 results back.
+carries a row's activations scaled by a power of two chosen from the
+row's largest magnitude (integer digits in the one-row GEMV, fp16 hi/lo
+pairs in the several-row GEMV, one fp16 rounding in the skinny and prefill
+GEMMs), and scales the fp32 results back.
 
 Checked at the BASELINE shapes (c0-c4) on every path: the decode GEMV (one
 and several activation rows), the skinny GEMM with and without split K, the
@@ -11,9 +12,11 @@ reading fp32 x directly (no workspace):
   - scaling x by a power of two scales y exactly (the row exponent moves,
     nothing else: a size-independent property, checked on every output):
     y(x * 2^k) = y(x) * 2^k for k in {-24, -16, -8, 8} on the GEMMs, whose
-    fp16 copy is always scaled; the decode GEMV keeps scale 1 for rows whose
-    largest |x| lies in [2^-10, 2^15), so there the relation is checked
-    between scalings outside that window (2^-24 vs 2^-16, 2^20 vs 2^28);
+    fp16 copy is always scaled, and on the one-row GEMV at c0-c2, whose
+    integer digits always take the slice's exponent; the several-row GEMV
+    keeps scale 1 for rows whose largest |x| lies in [2^-10, 2^15), so
+    there the relation is checked between scalings outside that window
+    (2^-24 vs 2^-16, 2^20 vs 2^28);
   - the scaled results and rows holding +-1e5 meet the oracle within the
     stated tolerance (|dy| <= 1e-3 ||x_row|| sqrt(K / 4096) or 2e-3 |y_ref|);
   - no output is NaN or inf (before, |x| >= 65520 turned whole rows NaN)."""
@@ -94,6 +97,9 @@ def test_any_finite_activation_range(pkg, oracle, cuda, case):
         if path == "auto" and m <= pkg.GEMV_MAX_ROWS:  # the decode GEMV
             exact(ys[-24], ys[-16], -8)
             exact(ys[28], ys[20], 8)
+            if m == 1:  # integer digits: the exponent follows every scaling
+                for e in SCALES:
+                    exact(ys[e], y0, e)
         else:
             for e in SCALES:
                 exact(ys[e], y0, e)
