@@ -138,9 +138,13 @@ int mlq_quantize_act_q8_0(const float* x, int rows, int row_size, void* out,
 /* ---------------------------------------------------------------------- */
 
 /* Tiled weight (from the upload path). Picks the kernel family by m:
- *  m = 1..8 (decode): HBM-streaming GEMV. Codes decode exactly to fp16,
- *    activations enter as an fp16 hi+lo pair (two MFMA rows), each block's
- *    MFMA result is scaled by its fp16 scale in fp32: fp32-class accuracy.
+ *  m = 1..8 (decode): HBM-streaming GEMV, fp32-class accuracy. One row:
+ *    activations as integers (22 bits below the largest |x| of each K
+ *    slice, three fp16 digits), codes fed with their fp16 bias and the
+ *    bias removed on the matrix core, every block sum exact; several rows
+ *    (and one-row slices of more than 8 groups): codes decoded exactly to
+ *    fp16, activations as an fp16 hi+lo pair (two MFMA rows). Each block's
+ *    sum is scaled by its fp16 scale in fp32.
  *  m > 8 (prefill / batched): MFMA f16 GEMM on d*q pre-scaled to fp16 and
  *    fp16-rounded activations, fp32 accumulation (~1e-4 relative).
  * Replaces q80/q40/q41LinearKernel + their launchers
