@@ -203,6 +203,43 @@ def test_gemv_every_split(pkg, oracle, cuda, qtype, split):
         pkg.set_gemv_split(0)
 
 
+@pytest.mark.parametrize("qtype", ["q4_0", "q4_1"])
+@pytest.mark.parametrize("split", [0, 1, 4])
+def test_one_row_gemv_block_sums_exact(pkg, oracle, cuda, qtype, split):
+    """The one-row GEMV carries activations as integers in three fp16
+    digits and removes the codes' fp16 bias on the matrix core; every
+    product and partial sum of a block is an integer below 2^24, so a block
+    sum is exact. Pinned bit for bit: unit block scales (q4_1 mins 0) and
+    integer activations that are non-zero in one 32-element block only (at
+    every block position of a group, in several groups and K slices; the
+    slice's largest |x| from 2^3 to 2^22 - 1, so its exponent moves from
+    scaling up to none), where every output must equal the exact integer
+    dot product rounded once to fp32. A wrong digit, sign, bias constant or
+    lane-quarter sum breaks the equality."""
+    n, k = 48, 1024
+    blocks = make_blocks(qtype, n, k, seed=97)
+    blocks["d"] = 0x3C00  # 1.0
+    if qtype == "q4_1":
+        blocks["m"] = 0
+    w = oracle.dequantize(blocks, (n, k), qtype).astype(np.int64)  # q - 8 / q
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    rng = np.random.default_rng(5)
+    pkg.set_gemv_split(split)
+    try:
+        for blk in [0, 1, 2, 3, 5, 14, 22, 31]:
+            for top in [2 ** 3, 2 ** 12, 2 ** 22 - 1]:
+                _print_case(test="block_sums_exact", qtype=qtype, split=split, blk=blk, top=top)
+                xi = np.zeros(k, np.int64)
+                xi[32 * blk:32 * blk + 32] = rng.integers(-top, top + 1, 32)
+                xi[32 * blk + 7] = top
+                want = (w @ xi).astype(np.float32)
+                got = pkg.linear(tw, _dev(xi.astype(np.float32), cuda),
+                                 path=pkg.PATH_GEMV).cpu().numpy()
+                assert np.array_equal(got, want), (blk, top, np.abs(got - want).max())
+    finally:
+        pkg.set_gemv_split(0)
+
+
 @pytest.mark.parametrize("qtype", TYPES)
 def test_linear_1d_input_and_aos_path(pkg, oracle, cuda, qtype):
     n, k = 80, 544
