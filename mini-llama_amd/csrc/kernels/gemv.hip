@@ -341,10 +341,11 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
   // activation row) x 4 halves (the group's blocks)
   _Float16* xsa = (_Float16*)(wl + (size_t)2 * M * a.xstride * 2);
   float* part = (float*)(smem + (size_t)a.split * a.wave_lds);
-  // One activation row, at most kDigMaxDepth groups in flight (DIG): the
-  // digit records of the slice's groups, then (q4_1) four block sums per
-  // group.
-  constexpr bool DIG = MR == 1 && GW <= kDigMaxDepth;
+  // One activation row, every group of the slice in flight, at most
+  // kDigMaxDepth of them (DIG): the digit records of the slice's groups,
+  // then (q4_1) four block sums per group. (Ring slices keep the hi/lo
+  // pairs: their records would not fit LDS at the longest K.)
+  constexpr bool DIG = MR == 1 && GW <= kDigMaxDepth && !RING;
   unsigned char* arec = wl;
   float* ssum = (float*)(wl + (size_t)npad * kDigRec);
 
@@ -988,10 +989,7 @@ int max_depth(int type, int m) {
 }
 // Ring depths that compile without spills, per type and row class.
 int ring_depth_lo(int type, int m) { return type == MLQ_Q4_1 ? (m == 1 ? 3 : 2) : 4; }
-int ring_depth_hi(int type, int m) {
-  // (q8_0's one-row ring of 8 with the pre-scaled input would spill)
-  return type == MLQ_Q4_1 ? (m == 1 ? 4 : 2) : (type == MLQ_Q8_0 && m == 1) ? 7 : 8;
-}
+int ring_depth_hi(int type, int m) { return type == MLQ_Q4_1 ? (m == 1 ? 4 : 2) : 8; }
 
 // Ring depth for a slice of gw groups: the one that pads the slice least to
 // whole passes (padded groups cost decode and MFMA work on zeros), the
@@ -1015,11 +1013,13 @@ int padded_groups(int type, int m, int gw) {
   return (gw + rd - 1) / rd * rd;
 }
 
-// Whether the kernel a plan launches stages digits: one activation row and
-// at most kDigMaxDepth groups in flight (every ring; non-ring slices up to
-// that depth).
+// Whether the kernel a plan launches stages digits: one activation row,
+// every group of the slice in flight (no ring), at most kDigMaxDepth of
+// them. The digit records take 784 bytes a group against ~512 for hi/lo
+// pairs, so ring slices keep the pairs: the one-row GEMV then still reaches
+// K ~ 38K (70B-class down projections, K = 28672 .. 29568).
 bool dig_layout(int type, int m, int gw) {
-  return m == 1 && (gw <= kDigMaxDepth || gw > max_depth(type, m));
+  return m == 1 && gw <= kDigMaxDepth && gw <= max_depth(type, m);
 }
 
 size_t wave_lds_bytes(int type, int m, int gw) {
@@ -1141,7 +1141,7 @@ hipError_t launch_depth(const GemvArgs& a, const Plan& p, hipStream_t stream) {
       case 5: return launch_typed<QT, MR, 5, true>(a, p.lds, stream);
       case 6: return launch_typed<QT, MR, 6, true>(a, p.lds, stream);
       case 7: return launch_typed<QT, MR, 7, true>(a, p.lds, stream);
-      default: return launch_typed<QT, MR, (QT == MLQ_Q8_0 && MR == 1) ? 7 : 8, true>(a, p.lds, stream);
+      default: return launch_typed<QT, MR, 8, true>(a, p.lds, stream);
     }
     }
   }

@@ -203,6 +203,22 @@ def test_gemv_every_split(pkg, oracle, cuda, qtype, split):
         pkg.set_gemv_split(0)
 
 
+@pytest.mark.parametrize("qtype", TYPES)
+def test_one_row_gemv_long_k(pkg, oracle, cuda, qtype):
+    """One activation row at 70B-class K (Qwen2-72B's down projection, K =
+    29568: 231 groups, slices longer than the in-flight budget, the refill
+    ring) stays on the decode GEMV (a forced GEMV path raises when the
+    planner cannot fit a shape) and meets the stated tolerance."""
+    n, k = 40, 29568
+    _print_case(test="gemv_long_k", qtype=qtype, n=n, k=k)
+    blocks = make_blocks(qtype, n, k, seed=n + k)
+    x = make_x(1, k, seed=k + 1)
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    got = pkg.linear(tw, _dev(x[0], cuda), path=pkg.PATH_GEMV).cpu().numpy()
+    ref = oracle.linear(x, blocks, (n, k), qtype, threads=8)[0]
+    assert tolerance_ok(got, ref, x, k).all(), error_report(got, ref, x, k)
+
+
 @pytest.mark.parametrize("qtype", ["q4_0", "q4_1"])
 @pytest.mark.parametrize("split", [0, 1, 4])
 def test_one_row_gemv_block_sums_exact(pkg, oracle, cuda, qtype, split):
@@ -215,8 +231,10 @@ def test_one_row_gemv_block_sums_exact(pkg, oracle, cuda, qtype, split):
     slice's largest |x| from 2^3 to 2^22 - 1, so its exponent moves from
     scaling up to none), where every output must equal the exact integer
     dot product rounded once to fp32. A wrong digit, sign, bias constant or
-    lane-quarter sum breaks the equality."""
-    n, k = 48, 1024
+    lane-quarter sum breaks the equality. (K = 896: seven groups, so even
+    one K slice holds every group in flight, the path that stages digits;
+    ring slices keep fp16 hi/lo pairs.)"""
+    n, k = 48, 896
     blocks = make_blocks(qtype, n, k, seed=97)
     blocks["d"] = 0x3C00  # 1.0
     if qtype == "q4_1":
@@ -226,7 +244,7 @@ def test_one_row_gemv_block_sums_exact(pkg, oracle, cuda, qtype, split):
     rng = np.random.default_rng(5)
     pkg.set_gemv_split(split)
     try:
-        for blk in [0, 1, 2, 3, 5, 14, 22, 31]:
+        for blk in [0, 1, 2, 3, 5, 14, 22, 27]:
             for top in [2 ** 3, 2 ** 12, 2 ** 22 - 1]:
                 _print_case(test="block_sums_exact", qtype=qtype, split=split, blk=blk, top=top)
                 xi = np.zeros(k, np.int64)
