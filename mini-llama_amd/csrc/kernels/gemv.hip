@@ -64,9 +64,9 @@
 //    [2^-10, 2^15), else the power of two that puts it in [2^14, 2^15)), and
 //    scales the row's results by 2^-e before the slices combine (exact
 //    power-of-two steps).
-//  - One activation row with at most 8 groups per wave (every decode
-//    projection but the 18944-deep down projection, and c0-c2) runs integer
-//    digits instead (DIG): the slice is staged as X = round(x * 2^e) with e
+//  - One activation row with at most 8 groups per wave, all in flight
+//    (every decode projection but the 18944-deep down projection, and
+//    c0-c2) runs integer digits instead (DIG): the slice is staged as X = round(x * 2^e) with e
 //    from the slice's largest |x| (|X| <= 2^22), three base-256 digits per
 //    element as fp16 integers; the codes keep their fp16 bias (1024 + q or
 //    64 + q: no subtracts), and per group one chain of five MFMAs (every
