@@ -148,3 +148,38 @@ def test_rmsnorm_folded_gemv_range(pkg, oracle, cuda, qtype):
             assert np.isfinite(got).all(), (scale, pos)
             err = np.abs(got - ref).max()
             assert err <= 1e-4 * np.abs(ref).max() + 1e-6, (scale, pos, err)
+
+
+@pytest.mark.parametrize("qtype", ["q8_0", "q4_0", "q4_1"])
+def test_one_row_gemv_tiny_and_non_finite(pkg, oracle, cuda, qtype):
+    """One-row GEMV (integer-digit staging) at the ends of the fp32 range:
+    a row whose largest |x| lies below 2^-104 (its slice exponent would
+    exceed 126, so the values gain 2^64 first) scales exactly against the
+    same row at 2^-100 and meets the oracle; a NaN or an inf anywhere in
+    the row makes every output non-finite (the reference's fp32 loop
+    propagates them the same way), and a finite row after it is unharmed."""
+    n, k = 300, 4096
+    print(f"range one-row {qtype}", flush=True)
+    blocks = make_blocks(qtype, n, k, seed=k + 7)
+    tw = pkg.upload(qtype, blocks, n, k, device=cuda)
+    base = make_x(1, k, seed=k + 8)[0]
+
+    def run(x):
+        return pkg.linear(tw, _dev(x.astype(np.float32), cuda)).cpu().numpy()
+
+    x_tiny = (base * np.float32(2.0 ** -120)).astype(np.float32)
+    x_mid = (base * np.float32(2.0 ** -100)).astype(np.float32)
+    y_tiny, y_mid = run(x_tiny), run(x_mid)
+    want = (y_mid.astype(np.float64) * 2.0 ** -20).astype(np.float32)
+    assert np.array_equal(y_tiny, want), np.abs(y_tiny - want).max()
+    ref = oracle.linear(x_tiny[None], blocks, (n, k), qtype, threads=8)
+    assert tolerance_ok(y_tiny[None], ref, x_tiny[None], k).all(), \
+        error_report(y_tiny[None], ref, x_tiny[None], k)
+    for bad in (np.nan, np.inf, -np.inf):
+        x = base.copy()
+        x[1234] = bad
+        y = run(x)
+        assert not np.isfinite(y).any(), (bad, np.isfinite(y).sum())
+    y = run(base)
+    ref = oracle.linear(base[None], blocks, (n, k), qtype, threads=8)
+    assert np.isfinite(y).all() and tolerance_ok(y[None], ref, base[None], k).all()
