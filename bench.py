@@ -832,6 +832,24 @@ def main():
     if args.mode == "headline":
         print(json.dumps({"mode": "headline", **head}), flush=True)
         return
+    # every other BASELINE config (GEMV / skinny shapes), a few seconds each,
+    # measured right after the headline, before the GEMM-heavy workloads:
+    # taken after the prefill and decode runs the same GEMVs read slower for
+    # a while (one box: c2 9.07 vs 8.48 us, c0 5.10 vs 4.97)
+    extra = {}
+    for name, qt, m, n, k in [("c0", "q8_0", 1, 4096, 4096),
+                              ("c2", "q4_1", 1, 4096, 14336),
+                              ("c3_m4", "q4_0", 4, 4096, 4096),
+                              ("c3_m16", "q4_0", 16, 4096, 4096),
+                              ("c3_m64", "q4_0", 64, 4096, 4096),
+                              ("c3_m16_q8_0", "q8_0", 16, 4096, 4096),
+                              ("c3_m64_q8_0", "q8_0", 64, 4096, 4096),
+                              ("c3_m16_q4_1", "q4_1", 16, 4096, 4096),
+                              ("c3_m64_q4_1", "q4_1", 64, 4096, 4096)]:
+        r = bench_case(pkg, torch, qt, m, n, k, args.steps, args.warmup, 100)
+        extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
+                       for kk, v in r.items()}
+        extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
     pre_steps = max(10, min(200, args.steps // 5))
     prefill = bench_case(pkg, torch, "q8_0", 512, 11008, 4096, pre_steps,
                          min(args.warmup, 5), seed=4000)
@@ -892,21 +910,6 @@ def main():
     except Exception as e:  # reported, never fatal to the headline line
         result["prefill_q8_0"] = {"error": f"{type(e).__name__}: {e}"}
     torch.cuda.empty_cache()
-    # every other BASELINE config (GEMV / skinny shapes), a few seconds each
-    extra = {}
-    for name, qt, m, n, k in [("c0", "q8_0", 1, 4096, 4096),
-                              ("c2", "q4_1", 1, 4096, 14336),
-                              ("c3_m4", "q4_0", 4, 4096, 4096),
-                              ("c3_m16", "q4_0", 16, 4096, 4096),
-                              ("c3_m64", "q4_0", 64, 4096, 4096),
-                              ("c3_m16_q8_0", "q8_0", 16, 4096, 4096),
-                              ("c3_m64_q8_0", "q8_0", 64, 4096, 4096),
-                              ("c3_m16_q4_1", "q4_1", 16, 4096, 4096),
-                              ("c3_m64_q4_1", "q4_1", 64, 4096, 4096)]:
-        r = bench_case(pkg, torch, qt, m, n, k, args.steps, args.warmup, 100)
-        extra[name] = {kk: (round(v, 3) if isinstance(v, float) else v)
-                       for kk, v in r.items()}
-        extra[name]["frac_hbm"] = round(r["gbs"] / HBM_PEAK_GBS, 4)
     # "LLC-hot": one weight copy, resident in the 256 MB Infinity Cache after
     # the warm-up launches; not an HBM figure
     hot = {}
