@@ -527,13 +527,6 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       }
     }
   };
-  // Rows whose largest |x| lies in [2^-10, 2^15) (the common case) keep
-  // scale 1: hi stays finite and the lo part's fp16 subnormal floor (2^-25)
-  // is below 2^-15 of the row's largest element, far inside the stated
-  // tolerance. The slice is staged with scale 1 right away while a
-  // wave-wide vote checks the window; only when a row falls outside it do
-  // the rows pay for their exact maxima (a cross-lane reduction) and a
-  // second, scaled staging pass. Returns whether every row kept scale 1.
   // One activation row (DIG): the slice is staged once as integers
   // X = round(x * 2^e), e from the slice's largest |x| (2^21 <= |X| max
   // < 2^22: 22 bits below the slice's largest element, any finite fp32 x,
@@ -569,6 +562,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvArgs a) {
       }
     }
   };
+  // Rows whose largest |x| lies in [2^-10, 2^15) (the common case) keep
+  // scale 1: hi stays finite and the lo part's fp16 subnormal floor (2^-25)
+  // is below 2^-15 of the row's largest element, far inside the stated
+  // tolerance. The slice is staged with scale 1 right away while a
+  // wave-wide vote checks the window; only when a row falls outside it do
+  // the rows pay for their exact maxima (a cross-lane reduction) and a
+  // second, scaled staging pass. Returns whether every row kept scale 1
+  // (the DIG path, which always scales: false).
   auto stage_slice = [&]() __attribute__((always_inline)) {
     if constexpr (norm) {
 #pragma unroll
